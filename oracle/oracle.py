@@ -1,0 +1,393 @@
+"""Python face of the CPU oracle (test infrastructure only).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` import this module.  It wraps ``liboracle.so`` (built from
+``gefen_oracle.c`` by ``oracle/Makefile``) and adds the pure-Python parts of
+the reference algorithm that are integer logic or small host code:
+
+* ``divisors`` (partitioning.py:13-30), ``largest_divisor_at_most``
+  (gefen.py:72-82);
+* ``finalize_period`` (partitioning.py:277-347) and ``find_period``
+  (partitioning.py:119-167 + gefen.py:812-828);
+* ``learn_codebook`` (gefen.py:305-419: histograms, fp32 accumulation, DP);
+* ``newton_schulz`` (gefen_muon.py:16-51) in float64 with a bf16 rounding of
+  every torch op output, and ``adjust_lr`` (gefen_muon.py:54-67);
+* ``GefenOracle`` / ``GefenMuonOracle``: whole optimizer steps on numpy arrays,
+  following ``Gefen.step`` / ``GefenMuon.step`` on the CPU path.
+
+Arrays of dtype 'bf16' and 'f16' are held as uint16 bit patterns.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+DT = {"f32": 0, "f16": 1, "bf16": 2}
+NP_STORAGE = {"f32": np.float32, "f16": np.uint16, "bf16": np.uint16}
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = HERE / "liboracle.so"
+        if not path.exists():
+            raise RuntimeError("oracle/liboracle.so is not built (run make -C oracle)")
+        L = ctypes.CDLL(str(path))
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        D = ctypes.c_double
+        I = ctypes.c_int
+        L.orc_gefen_step.argtypes = [I, I, P, P, P, P, P, I64, I64, I64, P, I, D, D, D, D, D, D, D, I]
+        L.orc_vmean_update.argtypes = [I, P, I, P, I64, I64, D]
+        L.orc_nearest.argtypes = [P, I, P, P, I64]
+        L.orc_histogram.argtypes = [I, P, I64, I64, I, P]
+        L.orc_accumulate_counts.argtypes = [P, P, I]
+        L.orc_exact_dp.argtypes = [P, I, I, I, P]
+        L.orc_period_scores.argtypes = [I, P, I64, P, I, I, D, P]
+        L.orc_muon_momentum.argtypes = [I, I, P, P, P, P, I64, I64, P, I, D, I]
+        L.orc_f32_to_bf16.argtypes = [P, P, I64]
+        L.orc_f32_to_f16.argtypes = [P, P, I64]
+        L.orc_fma32.argtypes = [P, ctypes.c_float, P, P, I64]
+        for name in ("orc_gefen_step", "orc_vmean_update", "orc_nearest", "orc_histogram",
+                     "orc_accumulate_counts", "orc_exact_dp", "orc_period_scores",
+                     "orc_muon_momentum", "orc_f32_to_bf16", "orc_f32_to_f16", "orc_fma32"):
+            getattr(L, name).restype = ctypes.c_int
+        _LIB = L
+    return _LIB
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data
+
+
+# ----------------------------------------------------------------- dtype helpers
+def to_f32(a: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "f32":
+        return np.asarray(a, dtype=np.float32)
+    if dtype == "bf16":
+        return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+    return np.asarray(a, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def from_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == "f32":
+        return x.copy()
+    out = np.empty(x.shape, dtype=np.uint16)
+    fn = lib().orc_f32_to_bf16 if dtype == "bf16" else lib().orc_f32_to_f16
+    fn(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def round_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    return to_f32(from_f32(x, dtype), dtype)
+
+
+# ----------------------------------------------------------------- partition logic
+def divisors(n: int, max_divisor: Optional[int] = None) -> List[int]:
+    """partitioning.py:13-30 (n itself included for n > 1, ascending)."""
+    if max_divisor is not None:
+        max_divisor = int(max_divisor)
+        if max_divisor < 1:
+            raise ValueError("max_divisor must be positive, got {}.".format(max_divisor))
+    small, large = [], []
+    for i in range(1, int(n ** 0.5) + 1):
+        if n % i == 0:
+            if i != n and (max_divisor is None or i <= max_divisor):
+                small.append(i)
+            paired = n // i
+            if i != paired and (max_divisor is None or paired <= max_divisor):
+                large.append(paired)
+    return small + large[::-1]
+
+
+def largest_divisor_at_most(value: int, limit: int) -> int:
+    """gefen.py:72-82."""
+    if value <= 0 or limit <= 0:
+        raise ValueError("expected positive value and limit")
+    if value <= limit:
+        return value
+    return divisors(value, max_divisor=limit)[-1]
+
+
+def finalize_period(periods_scores: Sequence[Tuple[int, float]], n: int) -> int:
+    """partitioning.py:277-347: best interior strict local maximum with p > 8,
+    capped to the smallest divisor of n in (1024, best] that divides best."""
+    if len(periods_scores) == 0:
+        raise ValueError("Expected at least one valid period candidate.")
+    last_period = periods_scores[-1][0]
+    cands = []
+    for i in range(1, len(periods_scores) - 1):
+        p, s = periods_scores[i]
+        if p <= 8 or p == last_period:
+            continue
+        if s <= periods_scores[i - 1][1] or s <= periods_scores[i + 1][1]:
+            continue
+        cands.append((s, p))
+    if not cands:
+        best = 1
+    else:
+        best_score, best = max(cands)
+        if not math.isfinite(best_score):
+            raise ValueError("Expected finite best score, got {}.".format(best_score))
+    if best > 1024:
+        best = min(p for p in divisors(n) if 1024 < p <= best and best % p == 0)
+    return best
+
+
+def period_scores(g: np.ndarray, dtype: str, divs: Sequence[int], mode: int = 1,
+                  eps: float = 1e-12) -> np.ndarray:
+    g = np.ascontiguousarray(g.reshape(-1))
+    d = np.ascontiguousarray(np.array(divs, dtype=np.int64))
+    out = np.empty(len(divs), dtype=np.float64)
+    rc = lib().orc_period_scores(DT[dtype], _ptr(g), g.size, _ptr(d), len(divs), mode, eps, _ptr(out))
+    if rc == 4:
+        raise ValueError("Expected values plus epsilon to be positive before log transform.")
+    if rc:
+        raise RuntimeError("orc_period_scores failed: {}".format(rc))
+    return out
+
+
+def find_period(g: np.ndarray, dtype: str, min_num_blocks: int = 4,
+                max_period: Optional[int] = None) -> int:
+    """Gefen._predict_period_from_grad_sq on the CPU backend (gefen.py:765-828)."""
+    n = int(np.asarray(g).size)
+    if n == 1:
+        return 1
+    divs = [p for p in divisors(n, max_divisor=max_period) if n // p >= min_num_blocks]
+    if not divs:
+        return 1
+    sc = period_scores(g, dtype, divs, mode=1)
+    return finalize_period(list(zip(divs, sc.tolist())), n)
+
+
+# ----------------------------------------------------------------- histogram / DP
+def histogram(g: np.ndarray, dtype: str, period: int, bins: int = 4096,
+              counts: Optional[np.ndarray] = None) -> np.ndarray:
+    g = np.ascontiguousarray(g.reshape(-1))
+    if counts is None:
+        counts = np.zeros(bins, dtype=np.int64)
+    rc = lib().orc_histogram(DT[dtype], _ptr(g), g.size, period, bins, _ptr(counts))
+    if rc:
+        raise ValueError("orc_histogram: bad period {} for numel {}".format(period, g.size))
+    return counts
+
+
+def exact_dp(counts_f32: np.ndarray, k: int = 256, force: bool = True) -> np.ndarray:
+    c = np.ascontiguousarray(counts_f32, dtype=np.float32)
+    out = np.empty(k, dtype=np.float32)
+    rc = lib().orc_exact_dp(_ptr(c), c.size, k, int(force), _ptr(out))
+    if rc == 2:
+        raise ValueError("Cannot run exact DP on an empty histogram.")
+    if rc:
+        raise RuntimeError("orc_exact_dp failed: {}".format(rc))
+    return out
+
+
+def learn_codebook(grad_periods: Sequence[Tuple[np.ndarray, str, int]], k: int = 256) -> Optional[np.ndarray]:
+    """gefen.py:305-419: per-tensor 4096-bin histograms, fp32 sum in order, exact DP."""
+    bins = k * 16
+    acc = np.zeros(bins, dtype=np.float32)
+    total = 0
+    for g, dtype, period in grad_periods:
+        cnt = histogram(g, dtype, period, bins)
+        lib().orc_accumulate_counts(_ptr(acc), _ptr(cnt), bins)
+        total += g.size
+    if total == 0:
+        return None
+    return exact_dp(acc, k, True)
+
+
+def nearest(cb: np.ndarray, x: np.ndarray) -> np.ndarray:
+    cb = np.ascontiguousarray(cb, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().orc_nearest(_ptr(cb), cb.size, _ptr(x), _ptr(out), x.size)
+    return out
+
+
+# ----------------------------------------------------------------- Newton-Schulz
+def newton_schulz_bf16(u_f32: np.ndarray, coeffs=(3.4445, -4.7750, 2.0315), steps: int = 5,
+                       eps: float = 1e-7) -> np.ndarray:
+    """gefen_muon.py:16-51 with float64 products and a bf16 rounding after every
+    torch op (input cast, norm, clamp, div_, each matmul / addmm)."""
+    a, b, c = coeffs
+    x = round_f32(u_f32.astype(np.float32), "bf16").astype(np.float64)
+    transposed = u_f32.shape[0] > u_f32.shape[1]
+    if transposed:
+        x = x.T.copy()
+    nrm = float(round_f32(np.array([np.sqrt(np.sum(x * x))], dtype=np.float32), "bf16")[0])
+    nrm = float(round_f32(np.array([max(nrm, np.float32(eps))], dtype=np.float32), "bf16")[0])
+    x = round_f32((x / nrm).astype(np.float32), "bf16").astype(np.float64)
+    for _ in range(steps):
+        A = round_f32((x @ x.T).astype(np.float32), "bf16").astype(np.float64)
+        B = round_f32((b * A + c * (A @ A)).astype(np.float32), "bf16").astype(np.float64)
+        x = round_f32((a * x + B @ x).astype(np.float32), "bf16").astype(np.float64)
+    if transposed:
+        x = x.T.copy()
+    return x.astype(np.float32)
+
+
+def adjust_lr(lr: float, adjust_lr_fn: Optional[str], shape) -> float:
+    """gefen_muon.py:54-67."""
+    rows, cols = shape[:2]
+    if adjust_lr_fn is None or adjust_lr_fn == "original":
+        ratio = math.sqrt(max(1, rows / cols))
+    elif adjust_lr_fn == "match_rms_adamw":
+        ratio = 0.2 * math.sqrt(max(rows, cols))
+    else:
+        ratio = 1.0
+    return lr * ratio
+
+
+# ----------------------------------------------------------------- optimizer state
+class TensorState:
+    def __init__(self, numel: int, period: int, dtype: str, sdtype: str):
+        self.period = period
+        self.step = 0
+        self.pod = largest_divisor_at_most(numel, 256) if period == 1 else None
+        mrows = numel // (self.pod if period == 1 else period)
+        self.m_codebook = np.zeros(numel, dtype=np.uint8)
+        self.m_magnitude = np.zeros(mrows, dtype=NP_STORAGE[sdtype])
+        self.vmean = np.zeros(numel // period, dtype=NP_STORAGE[sdtype])
+
+
+class GefenOracle:
+    """Gefen.step on the CPU path for a list of numpy parameters (gefen.py:1399-1420).
+
+    params: list of dicts {"p": array (storage dtype, updated in place), "dtype": str,
+    "shape": tuple, "lr", "beta1", "beta2", "eps", "weight_decay"}.
+    step(grads): one array or None per parameter.
+    """
+
+    def __init__(self, params: List[Dict], codebook: Optional[np.ndarray] = None, nthreads: int = 0):
+        self.params = params
+        self.codebook = None if codebook is None else np.ascontiguousarray(codebook, dtype=np.float32)
+        self.periods: List[Optional[int]] = [None] * len(params)
+        self.state: List[Optional[TensorState]] = [None] * len(params)
+        self.nthreads = nthreads
+        self.global_step = 0
+
+    def _predict(self, i: int, g: np.ndarray) -> int:
+        # gefen.py:908-913 / 1232-1257: reuse a stored period, numel 1 -> 1, else predict
+        if self.periods[i] is None:
+            self.periods[i] = 1 if g.size == 1 else find_period(g, self.params[i]["dtype"])
+        return self.periods[i]
+
+    def refresh_codebook(self, grads: Sequence[Optional[np.ndarray]]) -> None:
+        """_maybe_refresh_gefen_codebook (gefen.py:969-980)."""
+        if self.codebook is not None:
+            return
+        gp = []
+        for i, g in enumerate(grads):
+            if g is None or g.size == 0:
+                continue
+            gp.append((g, self.params[i]["dtype"], self._predict(i, g)))
+        self.codebook = learn_codebook(gp)
+
+    def _ensure_state(self, i: int, g: np.ndarray) -> TensorState:
+        if self.state[i] is None:
+            dt = self.params[i]["dtype"]
+            self.state[i] = TensorState(g.size, self._predict(i, g), dt, dt)
+        return self.state[i]
+
+    def step(self, grads: Sequence[Optional[np.ndarray]]) -> None:
+        self.refresh_codebook(grads)
+        for i, (prm, g) in enumerate(zip(self.params, grads)):
+            if g is None or g.size == 0:
+                continue
+            dt = prm["dtype"]
+            st = self._ensure_state(i, g)
+            st.step += 1
+            b1, b2 = prm["beta1"], prm["beta2"]
+            bc1 = 1 - b1 ** st.step
+            bc2 = 1 - b2 ** st.step
+            p = prm["p"]
+            gg = np.ascontiguousarray(g.reshape(-1))
+            rc = lib().orc_gefen_step(
+                DT[dt], DT[dt], _ptr(p), _ptr(gg), _ptr(st.m_codebook), _ptr(st.m_magnitude),
+                _ptr(st.vmean), gg.size, st.period, st.pod or 0, _ptr(self.codebook),
+                self.codebook.size, b1, b2, prm["lr"], prm["eps"], prm["weight_decay"],
+                bc1, bc2, self.nthreads)
+            if rc:
+                raise RuntimeError("orc_gefen_step failed: {}".format(rc))
+        self.global_step += 1
+
+
+def muon_momentum(g: np.ndarray, dtype: str, st: TensorState, codebook: np.ndarray,
+                  momentum: float, nesterov: bool) -> np.ndarray:
+    gg = np.ascontiguousarray(g.reshape(-1))
+    out = np.empty(gg.shape, dtype=NP_STORAGE[dtype])
+    mblk = st.pod if st.period == 1 else st.period
+    rc = lib().orc_muon_momentum(DT[dtype], DT[dtype], _ptr(gg), _ptr(st.m_codebook), _ptr(st.m_magnitude),
+                                 _ptr(out), gg.size, mblk, _ptr(codebook), codebook.size,
+                                 momentum, int(nesterov))
+    if rc:
+        raise RuntimeError("orc_muon_momentum failed: {}".format(rc))
+    return out
+
+
+class GefenMuonOracle(GefenOracle):
+    """GefenMuon.step on the CPU path (gefen_muon.py:216-350)."""
+
+    def __init__(self, params: List[Dict], codebook: Optional[np.ndarray] = None, momentum=0.95,
+                 nesterov=True, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7,
+                 adjust_lr_fn=None):
+        super().__init__(params, codebook)
+        self.momentum = momentum
+        self.nesterov = nesterov
+        self.ns = (ns_coefficients, ns_steps, eps)
+        self.adjust_lr_fn = adjust_lr_fn
+
+    def step(self, grads: Sequence[Optional[np.ndarray]]) -> None:
+        self.refresh_codebook(grads)
+        for i, (prm, g) in enumerate(zip(self.params, grads)):
+            if g is None or g.size == 0:
+                continue
+            dt = prm["dtype"]
+            st = self._ensure_state(i, g)
+            upd = muon_momentum(g, dt, st, self.codebook, self.momentum, self.nesterov)
+            st.step += 1
+            shape = prm["shape"]
+            u32 = to_f32(upd, dt).reshape(shape)
+            coeffs, steps, eps = self.ns
+            U = newton_schulz_bf16(u32, coeffs, steps, eps)
+            lr = prm["lr"]
+            adj = adjust_lr(lr, self.adjust_lr_fn, shape)
+            p = prm["p"]
+            pf = to_f32(p, dt).reshape(-1)
+            if prm["weight_decay"] > 0.0:
+                pf = round_f32(pf * np.float32(1 - lr * prm["weight_decay"]), dt)
+            Uf = np.ascontiguousarray(U.reshape(-1))
+            if dt == "f32":
+                # p.add_(U, alpha): promote(f32, bf16) = f32, one fused multiply-add
+                newp = _fma32(Uf, np.float32(-adj), pf)
+            else:
+                # reduced-float add_ with alpha rounded to the dtype.  The update of a
+                # tall matrix (rows > cols) is a transposed view, which takes the
+                # element-wise path where the product is rounded to the dtype too.
+                al = round_f32(np.array([-adj], dtype=np.float32), dt)[0]
+                prod = (Uf * al).astype(np.float32)
+                if shape[0] > shape[1]:
+                    prod = round_f32(prod, dt)
+                newp = round_f32((pf + prod).astype(np.float32), dt)
+            p[...] = from_f32(newp, dt).reshape(p.shape)
+        self.global_step += 1
+
+
+def _fma32(a: np.ndarray, b: np.float32, c: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().orc_fma32(_ptr(a), ctypes.c_float(b), _ptr(c), _ptr(out), a.size)
+    return out
