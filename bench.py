@@ -1,0 +1,282 @@
+"""Gefen optimizer-step benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama8b|llama1.5b|gpt2|muon]
+
+Prints ONE JSON line.  The default workload is BASELINE.json's north star: a
+Llama-3-8B-shaped parameter set (291 tensors, 8.03e9 bf16 parameters, bf16
+gradients, untied embed / lm_head).  Inputs are synthetic (integer-exact
+generator, gefen_amd/synthetic.py) and created in HBM before timing:
+parameters ~ N(0, 0.02), gradients ~ N(0, 1) times a per-tensor dyadic
+log-uniform scale in [2^-17, 2^-7] (~[1e-5, 1e-2]).
+
+* value / ms_per_step: median wall time of one ``optimizer.step()`` over the
+  timed steps (synchronised per step), steady state (steps after the first).
+* roofline: algorithmic HBM bytes of one step (p read+write, g read, 8-bit
+  index read+write, per-block state read+write with the chosen periods) divided
+  by the GPU time of the fused step kernels, measured with HIP events on the
+  launch stream around ``gefen_step_tasks``.
+* cpu_baseline: the CPU oracle (C restatement of the reference CPU path,
+  OpenMP) on a bounded sample of the same tensors, scaled to a full step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "optimizer step ms at GPT-2 125M / Llama-1.5B / 8B shapes; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def llama_shapes(hidden, layers, q_out, kv_out, inter, vocab):
+    shapes = [("embed_tokens", (vocab, hidden))]
+    for i in range(layers):
+        pre = "layers.{}.".format(i)
+        shapes += [(pre + "self_attn.q_proj", (q_out, hidden)), (pre + "self_attn.k_proj", (kv_out, hidden)),
+                   (pre + "self_attn.v_proj", (kv_out, hidden)), (pre + "self_attn.o_proj", (hidden, q_out)),
+                   (pre + "mlp.gate_proj", (inter, hidden)), (pre + "mlp.up_proj", (inter, hidden)),
+                   (pre + "mlp.down_proj", (hidden, inter)), (pre + "input_layernorm", (hidden,)),
+                   (pre + "post_attention_layernorm", (hidden,))]
+    shapes += [("norm", (hidden,)), ("lm_head", (vocab, hidden))]
+    return shapes
+
+
+def gpt2_shapes():
+    shapes = [("wte", (50257, 768)), ("wpe", (1024, 768))]
+    for i in range(12):
+        pre = "h.{}.".format(i)
+        shapes += [(pre + "attn.c_attn.weight", (768, 2304)), (pre + "attn.c_attn.bias", (2304,)),
+                   (pre + "attn.c_proj.weight", (768, 768)), (pre + "mlp.c_fc.weight", (768, 3072)),
+                   (pre + "mlp.c_proj.weight", (3072, 768)), (pre + "ln_1.weight", (768,)),
+                   (pre + "ln_1.bias", (768,)), (pre + "ln_2.weight", (768,)), (pre + "ln_2.bias", (768,))]
+    shapes += [("ln_f.weight", (768,))]
+    return shapes
+
+
+def qwen_muon_shapes():
+    shapes = []
+    for i in range(28):
+        pre = "layers.{}.".format(i)
+        shapes += [(pre + "q_proj", (2048, 2048)), (pre + "k_proj", (1024, 2048)), (pre + "v_proj", (1024, 2048)),
+                   (pre + "o_proj", (2048, 2048)), (pre + "gate_proj", (6144, 2048)), (pre + "up_proj", (6144, 2048)),
+                   (pre + "down_proj", (2048, 6144))]
+    return shapes
+
+
+CONFIGS = {
+    "llama8b": dict(shapes=lambda: llama_shapes(4096, 32, 4096, 1024, 14336, 128256), dtype=torch.bfloat16,
+                    grad="tensor", opt="gefen",
+                    workload="Llama-3-8B-shaped Gefen step: 291 tensors, 8.03e9 bf16 params + bf16 grads"),
+    "llama1.5b": dict(shapes=lambda: llama_shapes(2048, 16, 2048, 512, 8192, 128256), dtype=torch.bfloat16,
+                      grad="tensor", opt="gefen",
+                      workload="Llama-3-1.5B-shaped Gefen step: 147 tensors, 1.50e9 bf16 params + bf16 grads"),
+    "gpt2": dict(shapes=gpt2_shapes, dtype=torch.float32, grad="row", opt="gefen",
+                 workload="GPT-2 124M Gefen step: 111 fp32 tensors, row-scaled grads"),
+    "muon": dict(shapes=qwen_muon_shapes, dtype=torch.bfloat16, grad="muon", opt="muon",
+                 workload="GefenMuon step on Qwen3-1.7B-shaped 2D matrices (196 tensors, bf16)"),
+}
+PUBLISHED_MS = {"gpt2": 3.0, "llama1.5b": 29.0}  # README.md:142-145 (hardware not stated)
+
+
+def build_problem(cfg, dev, seed=2026):
+    from gefen_amd import synthetic as syn
+
+    params = []
+    for i, (name, shape) in enumerate(cfg["shapes"]()):
+        p = torch.empty(shape, dtype=cfg["dtype"], device=dev)
+        syn.fill_device(p, seed, 1_000_000 + i, syn.KIND_NORMAL, mult=0.02)
+        g = torch.empty(shape, dtype=cfg["dtype"], device=dev)
+        n = g.numel()
+        if cfg["grad"] == "row":
+            cols = shape[-1] if len(shape) > 1 else n
+            syn.fill_device(g, seed, i, syn.KIND_ROW_SCALED, cols=cols, e_lo=-14, e_hi=-4)
+        elif cfg["grad"] == "muon":
+            syn.fill_device(g, seed, i, syn.KIND_ROW_SCALED, cols=n, e_lo=-10, e_hi=-10)
+        else:
+            syn.fill_device(g, seed, i, syn.KIND_ROW_SCALED, cols=n, e_lo=-17, e_hi=-7)
+        p.requires_grad_(True)
+        p.grad = g
+        params.append((name, p))
+    torch.cuda.synchronize()
+    return params
+
+
+def step_bytes(opt, params):
+    """Algorithmic HBM bytes of one steady-state step with the chosen periods."""
+    total = 0
+    for _, p in params:
+        st = opt.state[p]
+        n = p.numel()
+        sd = p.element_size()
+        ss = st["m_magnitude"].element_size()
+        P = st["automatic_period"]
+        if P > 1:
+            total += n * (3 * sd + 2) + (n // P) * 2 * (ss + ss)
+        else:
+            d = st["period_one_divisor"]
+            total += n * (3 * sd + 2 + 2 * ss) + (n // d) * 2 * ss
+    return total
+
+
+def kernel_tasks(opt, params):
+    """The task array the optimizer passes to gefen_step_tasks (for direct timing)."""
+    from gefen_amd import _lib
+
+    tasks = np.zeros(len(params), dtype=_lib.STEP_TASK)
+    for i, (_, p) in enumerate(params):
+        st = opt.state[p]
+        g = opt.param_groups[i]
+        t = tasks[i]
+        t["p"], t["grad"] = p.data_ptr(), p.grad.data_ptr()
+        t["m_codebook"], t["m_magnitude"], t["vmean"] = (st["m_codebook"].data_ptr(), st["m_magnitude"].data_ptr(),
+                                                         st["vmean"].data_ptr())
+        t["numel"], t["period"] = p.numel(), st["automatic_period"]
+        t["period_one_divisor"] = st.get("period_one_divisor", 0) if st["automatic_period"] == 1 else 0
+        code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+        t["param_dtype"] = code[p.dtype]
+        t["state_dtype"] = code[st["m_magnitude"].dtype]
+        t["beta1"], t["beta2"], t["lr"], t["eps"], t["weight_decay"] = (g["beta1"], g["beta2"], g["lr"], g["eps"],
+                                                                         g["weight_decay"])
+        t["bias_correction_1"] = 1 - g["beta1"] ** (st["step"] + 1)
+        t["bias_correction_2"] = 1 - g["beta2"] ** (st["step"] + 1)
+    return tasks
+
+
+def cpu_baseline(opt, params, budget_s=20.0):
+    """Oracle (reference CPU path restated in C, OpenMP over blocks) on a sample
+    of the tensors, scaled by bytes to one full step."""
+    from oracle import oracle as orc
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cb = opt._gefen_codebook.detach().cpu().numpy().astype(np.float32)
+    # a contiguous run of transformer tensors (the embedding first in the list is skipped)
+    sample, sample_elems = [], 0
+    target = 60_000_000  # elements in the sample
+    for i in range(1, len(params)):
+        sample.append(i)
+        sample_elems += params[i][1].numel()
+        if sample_elems >= target:
+            break
+    host = []
+    for i in sample:
+        _, p = params[i]
+        st = opt.state[p]
+        conv = (lambda t: t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+                if t.dtype != torch.float32 else t.detach().contiguous().cpu().numpy().reshape(-1))
+        host.append((i, conv(p), conv(p.grad), st["m_codebook"].cpu().numpy().reshape(-1).copy(),
+                     conv(st["m_magnitude"]), conv(st["vmean"])))
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+    reps, elapsed = 0, 0.0
+    while elapsed < budget_s / 2 and reps < 50:
+        t0 = time.perf_counter()
+        for i, pp, gg, idx, mag, vm in host:
+            _, p = params[i]
+            st = opt.state[p]
+            g = opt.param_groups[i]
+            P = st["automatic_period"]
+            rc = orc.lib().orc_gefen_step(code[p.dtype], code[st["m_magnitude"].dtype], orc._ptr(pp), orc._ptr(gg),
+                                          orc._ptr(idx), orc._ptr(mag), orc._ptr(vm), p.numel(), P,
+                                          st.get("period_one_divisor", 0) if P == 1 else 0, orc._ptr(cb), cb.size,
+                                          g["beta1"], g["beta2"], g["lr"], g["eps"], g["weight_decay"], 0.5, 0.5, cores)
+            assert rc == 0
+        elapsed += time.perf_counter() - t0
+        reps += 1
+    per_rep = elapsed / reps
+    full = sum(p.numel() for _, p in params)
+    scaled_ms = per_rep * 1000.0 * full / sample_elems
+    return {"value": round(scaled_ms, 1), "unit": "ms per full step (scaled by elements)", "cores": cores,
+            "kind": "port",
+            "sample": "{} largest-first tensors, {:.3g} elements, {} repetitions of the oracle step "
+                      "(OpenMP over blocks), scaled to {:.3g} elements".format(len(sample), sample_elems, reps, full)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
+              "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    from gefen_amd.gefen import Gefen
+    from gefen_amd.gefen_muon import GefenMuon
+    from gefen_amd import _lib
+
+    params = build_problem(cfg, dev)
+    Opt = GefenMuon if cfg["opt"] == "muon" else Gefen
+    opt = Opt(params)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    opt.step()
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t0) * 1000.0
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        opt.step()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1000.0)
+    med = statistics.median(times)
+    q = np.percentile(times, [10, 90]).tolist()
+    out = {"metric": METRIC, "value": round(med, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(med, 4), "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16" if cfg["dtype"] == torch.bfloat16 else "f32", "data": "synthetic",
+           "config": {"workload": cfg["workload"], "tensors": len(params),
+                      "params": int(sum(p.numel() for _, p in params))},
+           "p10_ms": round(q[0], 4), "p90_ms": round(q[1], 4), "first_step_ms": round(first_ms, 1)}
+    if args.config in PUBLISHED_MS:
+        out["vs_baseline"] = round(PUBLISHED_MS[args.config] / med, 3)
+    periods = {}
+    for _, p in params:
+        P = opt.state[p]["automatic_period"]
+        periods[P] = periods.get(P, 0) + 1
+    out["config"]["periods"] = {str(k): v for k, v in sorted(periods.items())}
+    if cfg["opt"] == "gefen":
+        # fused step kernels alone, HIP events on the launch stream
+        tasks = kernel_tasks(opt, [(n, p) for n, p in params])
+        tables = opt._codebook_tables()
+        lib = _lib.load()
+        stream = torch.cuda.current_stream()
+        for _ in range(2):
+            _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream))
+        reps = max(args.steps, 5)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kms = e0.elapsed_time(e1) / reps
+        nbytes = step_bytes(opt, params)
+        achieved = nbytes / (kms * 1e-3) / 1e9
+        out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                           "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes)}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline(opt, params)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

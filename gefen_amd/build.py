@@ -1,0 +1,83 @@
+"""Build libgefen_hip.so (the C-ABI library) and libgefen_synth.so in-tree.
+
+    python -m gefen_amd.build [--jobs N]
+
+hipcc cross-compiles for gfx950 without a GPU.  Flags:
+  -ffp-contract=off        only the fused multiply-adds written in the source
+                           are fused (the reference CPU path rounds every op);
+  -packed-fp32-ops off     no v_pk_*_f32 code generation.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = os.environ.get("GEFEN_OFFLOAD_ARCH", "gfx950")
+
+COMMON = [
+    "--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-result",
+    "-I", str(REPO / "include"), "-I", str(CSRC),
+]
+
+LIBS = {
+    "libgefen_hip.so": ["capi.cpp", "step.hip", "codebook.hip", "period.hip"],
+    "libgefen_synth.so": ["capi.cpp", "synthetic.hip"],
+}
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [HIPCC] + COMMON + ["-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cmd = [HIPCC] + COMMON + ["-x", "hip", "-c", str(src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed on {}".format(src.name))
+    noise = "is not a recognized feature for this target"
+    msgs = [ln for ln in (r.stdout + r.stderr).splitlines() if ln.strip() and noise not in ln]
+    if msgs:
+        sys.stderr.write("\n".join(msgs) + "\n")
+
+
+def build(jobs: int = 8, only=None) -> None:
+    BUILD.mkdir(exist_ok=True)
+    for lib, srcs in LIBS.items():
+        if only and lib not in only:
+            continue
+        objs = []
+        todo = []
+        for s in srcs:
+            src = CSRC / s
+            obj = BUILD / (s + ".o")
+            objs.append(obj)
+            todo.append((src, obj))
+        with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+            list(ex.map(lambda a: _compile(*a), todo))
+        out = PKG / lib
+        tmp = PKG / (lib + ".tmp")
+        cmd = [HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", str(tmp)] + [str(o) for o in objs]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError("link failed for {}".format(lib))
+        os.replace(tmp, out)
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=8)
+    args = ap.parse_args()
+    build(args.jobs)
+    print("built", ", ".join(LIBS))

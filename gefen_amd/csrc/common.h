@@ -1,0 +1,115 @@
+// Shared device helpers for the Gefen HIP kernels (gfx950 / CDNA4, wave64).
+//
+// Numerics follow the reference's CPU path (torch 2.10 CPU): every torch op
+// result is rounded to its tensor dtype (round to nearest even), lerp and
+// add(alpha=) are single fused multiply-adds, divisions are IEEE correctly
+// rounded.  Build with -ffp-contract=off: only the __builtin_fmaf calls written
+// here are fused.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gefen_hip.h"
+
+namespace gefen {
+
+// ----------------------------------------------------------------- dtypes
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return __uint_as_float((uint32_t)v.bits << 16); }
+__device__ __forceinline__ float to_f32(f16_t v) {
+    _Float16 h;
+    __builtin_memcpy(&h, &v.bits, 2);
+    return (float)h;
+}
+
+template <typename T> struct Conv;
+template <> struct Conv<float> {
+    __device__ __forceinline__ static float from(float v) { return v; }
+};
+template <> struct Conv<bf16_t> {
+    __device__ __forceinline__ static bf16_t from(float v) {
+        __bf16 b = (__bf16)v;  // v_cvt_pk_bf16_f32: round to nearest even
+        bf16_t r;
+        __builtin_memcpy(&r.bits, &b, 2);
+        return r;
+    }
+};
+template <> struct Conv<f16_t> {
+    __device__ __forceinline__ static f16_t from(float v) {
+        _Float16 h = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
+        f16_t r;
+        __builtin_memcpy(&r.bits, &h, 2);
+        return r;
+    }
+};
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) { return Conv<T>::from(v); }
+// value of v after a round trip through dtype T
+template <typename T>
+__device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+
+// NaN-propagating maximum of non-negative values (torch amax semantics)
+__device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
+
+// ----------------------------------------------------------------- vector access
+// W consecutive elements of type T moved with one load/store of W*sizeof(T) bytes.
+template <typename T, int W>
+struct alignas(sizeof(T) * W) Vec { T v[W]; };
+
+template <typename T, int W>
+__device__ __forceinline__ Vec<T, W> vload(const T* base, int64_t elem) {
+    return *reinterpret_cast<const Vec<T, W>*>(base + elem);
+}
+template <typename T, int W>
+__device__ __forceinline__ void vstore(T* base, int64_t elem, const Vec<T, W>& x) {
+    *reinterpret_cast<Vec<T, W>*>(base + elem) = x;
+}
+
+// ----------------------------------------------------------------- wave reductions
+// Butterfly over groups of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float group_max(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v = nanmax(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ----------------------------------------------------------------- codebook tables
+// Prepared once per codebook (gefen_prepare_codebook):
+//   cb[k]    codebook (sorted ascending), K <= 256 entries
+//   thr[k]   for k = 1..K-1 the largest float x in (cb[k-1], cb[k]] for which the
+//            reference's tie rule |x - cb[k-1]| <= |x - cb[k]| (fp32 differences)
+//            picks the left entry, or cb[k-1] if none; thr[K] = +inf sentinel.
+//            The nearest index of a non-NaN x is #{k in 1..K-1 : thr[k] < x}.
+//   bucket[e] for e = 0..4096: #{k : thr[k] < -1 + e/2048}.
+struct CodebookTables {
+    float cb[256];
+    float thr[260];
+    uint16_t bucket[4100];
+    int32_t K;
+    int32_t pad[3];
+};
+
+// Nearest codebook index (gefen.py:122-143) from LDS copies of thr and bucket.
+__device__ __forceinline__ int nearest_index(float x, const float* thr, const uint16_t* bucket, int K) {
+    if (x != x) return K - 1;  // searchsorted(NaN) = K -> right = left = K-1
+    int k = 0;
+    if (x >= -1.0f) {
+        float y = fminf((x + 1.0f) * 2048.0f, 4096.0f);
+        int b = (int)y;  // y >= 0: truncation == floor
+        // x + 1 may round up across one bucket edge for x >= 0: step back if the
+        // edge (exact: a multiple of 2^-11 in [-1, 1]) exceeds x
+        if (-1.0f + (float)b * 0.00048828125f > x) b -= 1;
+        k = bucket[b];
+    }
+    while (k < K - 1 && thr[k + 1] < x) ++k;
+    return k;
+}
+
+}  // namespace gefen

@@ -1,0 +1,982 @@
+// Fused Gefen / GefenMuon update kernels for gfx950.
+//
+// One pass over the parameters, gradients and 8-bit codebook indices per step.
+// Work unit: a magnitude block ("row") of `rowlen` elements -- the automatic
+// period P, or the period-one divisor d when P = 1.  A row is owned by a group
+// of LPR lanes (LPR = power of two <= 64, so a wave64 holds 64/LPR rows); each
+// lane keeps up to R vectors of W elements in registers, so the row is read
+// once, reduced with xor-butterflies inside the lane group (absmax for the
+// magnitude, sum of squares for vmean) and written once.  Rows longer than
+// 64*R*W elements take a two-sweep workgroup-per-row kernel.
+//
+// The arithmetic is the reference's CPU path (gefen.py:116-119, 1153-1206,
+// 1280-1281, 1326-1333; gefen_muon.py:132-171, 302-316), op by op.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "capi_internal.h"
+#include "common.h"
+
+namespace gefen {
+
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kIter = 4;       // wave-units per wave in one workgroup
+constexpr int kMaxBatch = 20;  // tasks per launch (kernel argument block < 4 KB)
+
+enum StepMode : int32_t { kVmeanUpdate = 0, kVmeanGiven = 1, kStepsizeGiven = 2 };
+
+struct StepTask {
+    void* p;
+    const void* g;
+    uint8_t* idx;
+    void* mag;
+    void* vmean;
+    const float* stepsize;
+    int64_t nrows;     // magnitude rows
+    int64_t rowlen;    // elements per magnitude row
+    int32_t period;    // elements per vmean row (rowlen if P > 1, 1 if P = 1)
+    int32_t nvec;      // rowlen / W (register path)
+    int32_t lpr_log2;  // log2(lanes per row)
+    int32_t mode;      // StepMode
+    float b1c, b2, omb2, sqrt_bc2, eps, inv_bc1, lr, wdf;
+    int32_t do_wd;
+    int32_t nwg;       // workgroups of this task
+};
+
+struct StepBatch {
+    StepTask t[kMaxBatch];
+    int32_t wg_begin[kMaxBatch + 1];
+    int32_t ntasks;
+    int32_t pad;
+    const CodebookTables* tables;
+};
+
+// LDS copy of the codebook tables, with the codebook rounded to the parameter dtype.
+struct LdsTables {
+    float cbd[256];
+    float thr[260];
+    uint16_t bucket[4100];
+};
+
+template <typename D>
+__device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* T, int& K) {
+    K = T->K;
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) L.cbd[i] = round_to<D>(T->cb[i]);
+    for (int i = threadIdx.x; i < 260; i += blockDim.x) L.thr[i] = T->thr[i];
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(T->bucket);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(L.bucket);
+    for (int i = threadIdx.x; i < 2050; i += blockDim.x) dst[i] = src[i];
+    __syncthreads();
+}
+
+__device__ __forceinline__ int find_task(const int32_t* wg_begin, int ntasks) {
+    int t = 0;
+    const int b = blockIdx.x;
+    while (t + 1 < ntasks && wg_begin[t + 1] <= b) ++t;
+    return t;
+}
+
+// stepsize of gefen.py:1326-1327: (1/bc1) * reciprocal(sqrt(v)/sqrt(bc2) + eps)
+__device__ __forceinline__ float stepsize_of(float v, const StepTask& T) {
+    float h = sqrtf(v) / T.sqrt_bc2 + T.eps;
+    return (1.0f / h) * T.inv_bc1;
+}
+
+// ---------------------------------------------------------------------------
+// Gefen step, register path.  QROUND: the dequantised update cb[idx]*mag is
+// rounded to D (param dtype == state dtype) or kept in fp32 (fp32 state).
+template <typename D, typename S, int W, int R, bool P1>
+__global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
+    __shared__ LdsTables L;
+    int K;
+    load_tables<D>(L, B.tables, K);
+    const int ti = find_task(B.wg_begin, B.ntasks);
+    const StepTask& T = B.t[ti];
+    constexpr bool QROUND = sizeof(D) == sizeof(S);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lpr = 1 << T.lpr_log2;
+    const int rpw = 64 >> T.lpr_log2;
+    const int lir = lane & (lpr - 1);
+    const int sub = lane >> T.lpr_log2;
+    const int64_t lw = blockIdx.x - B.wg_begin[ti];
+
+    D* __restrict__ p = static_cast<D*>(T.p);
+    const D* __restrict__ g = static_cast<const D*>(T.g);
+    uint8_t* __restrict__ idx = T.idx;
+    S* __restrict__ mag = static_cast<S*>(T.mag);
+    S* __restrict__ vm = static_cast<S*>(T.vmean);
+
+    for (int it = 0; it < kIter; ++it) {
+        const int64_t unit = (lw * kIter + it) * 4 + wave;
+        const int64_t row = unit * rpw + sub;
+        if (unit * rpw >= T.nrows) break;  // uniform across the wave
+        const bool active = row < T.nrows;
+        const int64_t base = row * T.rowlen;
+
+        Vec<D, W> gv[R], pv[R];
+        Vec<uint8_t, W> iv[R];
+        Vec<S, W> vv[R];
+        float upd[R][W];
+        float mx = 0.0f, sumsq = 0.0f;
+        const float mold = active ? to_f32(mag[row]) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = lir + j * lpr;
+            if (active && v < T.nvec) {
+                const int64_t e = base + (int64_t)v * W;
+                gv[j] = vload<D, W>(g, e);
+                iv[j] = vload<uint8_t, W>(idx, e);
+                pv[j] = vload<D, W>(p, e);
+                if (P1) vv[j] = vload<S, W>(vm, e);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = lir + j * lpr;
+            if (active && v < T.nvec) {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const float gf = to_f32(gv[j].v[w]);
+                    const float cur = L.cbd[iv[j].v[w]] * mold;
+                    const float u = __builtin_fmaf(T.b1c, gf - cur, cur);  // lerp, w < 0.5
+                    upd[j][w] = u;
+                    mx = nanmax(mx, fabsf(u));
+                    if (!P1) {
+                        const float sq = gf * gf;
+                        sumsq = sumsq + sq;
+                    }
+                }
+            }
+        }
+        mx = group_max(mx, lpr);
+        float ss = 0.0f;
+        if (!P1) {
+            if (T.mode == kVmeanUpdate) {
+                const float tot = group_sum(sumsq, lpr);
+                if (active) {
+                    const float ms = tot / (float)T.period;
+                    const float prev = to_f32(vm[row]) * T.b2;
+                    const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, prev));
+                    if (lir == 0) vm[row] = vnew;
+                    ss = stepsize_of(to_f32(vnew), T);
+                }
+            } else if (T.mode == kVmeanGiven) {
+                if (active) ss = stepsize_of(to_f32(vm[row]), T);
+            } else {
+                if (active) ss = T.stepsize[row];
+            }
+        }
+        if (!active) continue;
+        const S mag_s = from_f32<S>(mx);
+        if (lir == 0) mag[row] = mag_s;
+        const float mn = to_f32(mag_s);
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = lir + j * lpr;
+            if (v < T.nvec) {
+                const int64_t e = base + (int64_t)v * W;
+                Vec<uint8_t, W> io;
+                Vec<D, W> po;
+                Vec<S, W> vo;
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const float x = (mn > 0.0f) ? upd[j][w] / mn : 0.0f;
+                    const int k = nearest_index(x, L.thr, L.bucket, K);
+                    io.v[w] = (uint8_t)k;
+                    float q = L.cbd[k] * mn;
+                    if (QROUND) q = round_to<D>(q);
+                    float s = ss;
+                    if (P1) {
+                        const float gf = to_f32(gv[j].v[w]);
+                        const float sq = gf * gf;  // mean over a one-element row
+                        const float prev = to_f32(vv[j].v[w]) * T.b2;
+                        const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
+                        vo.v[w] = vnew;
+                        s = stepsize_of(to_f32(vnew), T);
+                    }
+                    const float u = (q * s) * T.lr;
+                    float pf = to_f32(pv[j].v[w]);
+                    if (T.do_wd) pf = round_to<D>(pf * T.wdf);
+                    po.v[w] = from_f32<D>(pf - u);
+                }
+                vstore<uint8_t, W>(idx, e, io);
+                vstore<D, W>(p, e, po);
+                if (P1) vstore<S, W>(vm, e, vo);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gefen step, two-sweep path for rows longer than the register path holds
+// (P > 1 only): one workgroup per row, the second sweep re-reads g and idx.
+template <typename D, typename S>
+__global__ __launch_bounds__(kThreads) void k_gefen_step_long(const StepBatch B) {
+    __shared__ LdsTables L;
+    __shared__ float red_mx[4], red_sum[4];
+    int K;
+    load_tables<D>(L, B.tables, K);
+    const int ti = find_task(B.wg_begin, B.ntasks);
+    const StepTask& T = B.t[ti];
+    constexpr bool QROUND = sizeof(D) == sizeof(S);
+    const int64_t row = blockIdx.x - B.wg_begin[ti];
+    if (row >= T.nrows) return;
+    D* __restrict__ p = static_cast<D*>(T.p);
+    const D* __restrict__ g = static_cast<const D*>(T.g);
+    uint8_t* __restrict__ idx = T.idx;
+    S* __restrict__ mag = static_cast<S*>(T.mag);
+    S* __restrict__ vm = static_cast<S*>(T.vmean);
+    const int64_t base = row * T.rowlen;
+    const float mold = to_f32(mag[row]);
+    float mx = 0.0f, sumsq = 0.0f;
+    for (int64_t j = threadIdx.x; j < T.rowlen; j += kThreads) {
+        const float gf = to_f32(g[base + j]);
+        const float cur = L.cbd[idx[base + j]] * mold;
+        const float u = __builtin_fmaf(T.b1c, gf - cur, cur);
+        mx = nanmax(mx, fabsf(u));
+        const float sq = gf * gf;
+        sumsq = sumsq + sq;
+    }
+    mx = group_max(mx, 64);
+    sumsq = group_sum(sumsq, 64);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { red_mx[wave] = mx; red_sum[wave] = sumsq; }
+    __syncthreads();
+    mx = nanmax(nanmax(red_mx[0], red_mx[1]), nanmax(red_mx[2], red_mx[3]));
+    const float tot = (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
+    float ss;
+    if (T.mode == kVmeanUpdate) {
+        const float ms = tot / (float)T.period;
+        const float prev = to_f32(vm[row]) * T.b2;
+        const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, prev));
+        ss = stepsize_of(to_f32(vnew), T);
+        __syncthreads();  // every thread has read vm[row] before it is replaced
+        if (threadIdx.x == 0) vm[row] = vnew;
+    } else if (T.mode == kVmeanGiven) {
+        ss = stepsize_of(to_f32(vm[row]), T);
+    } else {
+        ss = T.stepsize[row];
+    }
+    const S mag_s = from_f32<S>(mx);
+    const float mn = to_f32(mag_s);
+    __syncthreads();  // every thread has read mag[row] (mold) before it is replaced
+    if (threadIdx.x == 0) mag[row] = mag_s;
+    for (int64_t j = threadIdx.x; j < T.rowlen; j += kThreads) {
+        const float gf = to_f32(g[base + j]);
+        const float cur = L.cbd[idx[base + j]] * mold;
+        const float u = __builtin_fmaf(T.b1c, gf - cur, cur);
+        const float x = (mn > 0.0f) ? u / mn : 0.0f;
+        const int k = nearest_index(x, L.thr, L.bucket, K);
+        idx[base + j] = (uint8_t)k;
+        float q = L.cbd[k] * mn;
+        if (QROUND) q = round_to<D>(q);
+        const float uu = (q * ss) * T.lr;
+        float pf = to_f32(p[base + j]);
+        if (T.do_wd) pf = round_to<D>(pf * T.wdf);
+        p[base + j] = from_f32<D>(pf - uu);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GefenMuon quantised momentum (gefen_muon.py:302-316 with 132-171): every op is
+// a torch op on a D tensor, so each result is rounded to D.
+struct MuonTask {
+    const void* g;
+    uint8_t* idx;
+    void* mag;
+    void* out;
+    int64_t nrows;
+    int64_t rowlen;
+    int32_t nvec;
+    int32_t lpr_log2;
+    float w;       // f32(1 - momentum): lerp weight
+    float mom;     // f32(momentum)
+    float alpha;   // add_ alpha: f32(1 - momentum), rounded to D for reduced dtypes
+    float tiny;    // finfo(D).tiny rounded to S
+    int32_t nesterov;
+    int32_t nwg;
+};
+
+struct MuonBatch {
+    MuonTask t[kMaxBatch];
+    int32_t wg_begin[kMaxBatch + 1];
+    int32_t ntasks;
+    int32_t pad;
+    const CodebookTables* tables;
+};
+
+template <typename D, typename S>
+__device__ __forceinline__ float muon_out(float q, float gf, const MuonTask& T) {
+    if (!T.nesterov) return q;
+    const float a = round_to<D>(q * T.mom);  // mul_(momentum)
+    if (sizeof(D) == 4) return __builtin_fmaf(gf, T.alpha, a);  // add_(g, alpha): fma
+    return a + gf * T.alpha;  // reduced dtype: alpha in D, exact product, one rounding
+}
+
+template <typename D, typename S, int W, int R>
+__global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
+    __shared__ LdsTables L;
+    int K;
+    load_tables<D>(L, B.tables, K);
+    const int ti = find_task(B.wg_begin, B.ntasks);
+    const MuonTask& T = B.t[ti];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lpr = 1 << T.lpr_log2;
+    const int rpw = 64 >> T.lpr_log2;
+    const int lir = lane & (lpr - 1);
+    const int sub = lane >> T.lpr_log2;
+    const int64_t lw = blockIdx.x - B.wg_begin[ti];
+    const D* __restrict__ g = static_cast<const D*>(T.g);
+    uint8_t* __restrict__ idx = T.idx;
+    S* __restrict__ mag = static_cast<S*>(T.mag);
+    D* __restrict__ out = static_cast<D*>(T.out);
+
+    for (int it = 0; it < kIter; ++it) {
+        const int64_t unit = (lw * kIter + it) * 4 + wave;
+        const int64_t row = unit * rpw + sub;
+        if (unit * rpw >= T.nrows) break;
+        const bool active = row < T.nrows;
+        const int64_t base = row * T.rowlen;
+        Vec<D, W> gv[R];
+        Vec<uint8_t, W> iv[R];
+        float mu[R][W];
+        float mx = 0.0f;
+        const float mold = active ? to_f32(mag[row]) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = lir + j * lpr;
+            if (active && v < T.nvec) {
+                const int64_t e = base + (int64_t)v * W;
+                gv[j] = vload<D, W>(g, e);
+                iv[j] = vload<uint8_t, W>(idx, e);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = lir + j * lpr;
+            if (active && v < T.nvec) {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const float gf = to_f32(gv[j].v[w]);
+                    const float m0 = round_to<D>(L.cbd[iv[j].v[w]] * mold);         // dequant * mag
+                    const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));  // lerp_
+                    mu[j][w] = m1;
+                    mx = nanmax(mx, fabsf(m1));
+                }
+            }
+        }
+        mx = group_max(mx, lpr);
+        if (!active) continue;
+        const S mag_s = from_f32<S>(mx);
+        if (lir == 0) mag[row] = mag_s;
+        const float ms = to_f32(mag_s);
+        const float clamped = (ms < T.tiny) ? T.tiny : ms;  // clamp(min=tiny) in S
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = lir + j * lpr;
+            if (v < T.nvec) {
+                const int64_t e = base + (int64_t)v * W;
+                Vec<uint8_t, W> io;
+                Vec<D, W> oo;
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    float x = round_to<D>(mu[j][w] / clamped);  // div_
+                    if (ms <= 0.0f) x = 0.0f;                   // masked_fill_(mag <= 0)
+                    const int k = nearest_index(x, L.thr, L.bucket, K);
+                    io.v[w] = (uint8_t)k;
+                    const float q = round_to<D>(L.cbd[k] * ms);  // copy_(cb[idx]) then mul_(mag)
+                    oo.v[w] = from_f32<D>(muon_out<D, S>(q, to_f32(gv[j].v[w]), T));
+                }
+                vstore<uint8_t, W>(idx, e, io);
+                vstore<D, W>(out, e, oo);
+            }
+        }
+    }
+}
+
+template <typename D, typename S>
+__global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
+    __shared__ LdsTables L;
+    __shared__ float red_mx[4];
+    int K;
+    load_tables<D>(L, B.tables, K);
+    const int ti = find_task(B.wg_begin, B.ntasks);
+    const MuonTask& T = B.t[ti];
+    const int64_t row = blockIdx.x - B.wg_begin[ti];
+    if (row >= T.nrows) return;
+    const D* __restrict__ g = static_cast<const D*>(T.g);
+    uint8_t* __restrict__ idx = T.idx;
+    S* __restrict__ mag = static_cast<S*>(T.mag);
+    D* __restrict__ out = static_cast<D*>(T.out);
+    const int64_t base = row * T.rowlen;
+    const float mold = to_f32(mag[row]);
+    float mx = 0.0f;
+    for (int64_t j = threadIdx.x; j < T.rowlen; j += kThreads) {
+        const float gf = to_f32(g[base + j]);
+        const float m0 = round_to<D>(L.cbd[idx[base + j]] * mold);
+        const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));
+        mx = nanmax(mx, fabsf(m1));
+    }
+    mx = group_max(mx, 64);
+    if ((threadIdx.x & 63) == 0) red_mx[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = nanmax(nanmax(red_mx[0], red_mx[1]), nanmax(red_mx[2], red_mx[3]));
+    const S mag_s = from_f32<S>(mx);
+    const float ms = to_f32(mag_s);
+    const float clamped = (ms < T.tiny) ? T.tiny : ms;
+    __syncthreads();
+    if (threadIdx.x == 0) mag[row] = mag_s;
+    for (int64_t j = threadIdx.x; j < T.rowlen; j += kThreads) {
+        const float gf = to_f32(g[base + j]);
+        const float m0 = round_to<D>(L.cbd[idx[base + j]] * mold);
+        const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));
+        float x = round_to<D>(m1 / clamped);
+        if (ms <= 0.0f) x = 0.0f;
+        const int k = nearest_index(x, L.thr, L.bucket, K);
+        idx[base + j] = (uint8_t)k;
+        const float q = round_to<D>(L.cbd[k] * ms);
+        out[base + j] = from_f32<D>(muon_out<D, S>(q, gf, T));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// vmean only (automatic_vmean_update): one lane group per row, streaming.
+template <typename G, typename S>
+__global__ __launch_bounds__(kThreads) void k_vmean(S* __restrict__ vm, const G* __restrict__ g,
+                                                     int64_t nrows, int64_t period, int lpr_log2,
+                                                     float b2, float omb2) {
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int lir = lane & (lpr - 1);
+    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row = unit * (64 >> lpr_log2) + (lane >> lpr_log2);
+    const bool active = row < nrows;
+    float s = 0.0f;
+    if (active) {
+        const int64_t base = row * period;
+        for (int64_t j = lir; j < period; j += lpr) {
+            const float gf = to_f32(g[base + j]);
+            const float sq = gf * gf;
+            s = s + sq;
+        }
+    }
+    s = group_sum(s, lpr);
+    if (active && lir == 0) {
+        const float ms = s / (float)period;
+        const float prev = to_f32(vm[row]) * b2;
+        vm[row] = from_f32<S>(__builtin_fmaf(ms, omb2, prev));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+namespace {
+
+int lpr_log2_for(int64_t nvec) {
+    int l = 0;
+    while ((1LL << l) < nvec && l < 6) ++l;
+    return l;
+}
+
+int pick_width(int dsize, int64_t rowlen, std::initializer_list<const void*> ptrs, int idx_needed,
+               const void* idx_ptr, int ssize, const void* vptr) {
+    const int cands16[3] = {8, 4, 1};
+    const int cands32[2] = {4, 1};
+    const int* c = dsize == 2 ? cands16 : cands32;
+    const int nc = dsize == 2 ? 3 : 2;
+    for (int i = 0; i < nc; ++i) {
+        const int W = c[i];
+        if (rowlen % W) continue;
+        bool ok = true;
+        for (const void* q : ptrs) ok = ok && aligned(q, W * dsize);
+        if (idx_needed) ok = ok && aligned(idx_ptr, W);
+        if (vptr) ok = ok && aligned(vptr, W * ssize);
+        if (ok) return W;
+    }
+    return 1;
+}
+
+int r_bucket(int64_t nvec, int lpr_log2) {
+    const int64_t r = (nvec + (1LL << lpr_log2) - 1) >> lpr_log2;
+    if (r <= 1) return 1;
+    if (r <= 2) return 2;
+    if (r <= 4) return 4;
+    if (r <= 8) return 8;
+    return 0;  // two-sweep path
+}
+
+// kernel key: dtype pair, W, R (0 = long rows), P1
+struct Key {
+    int d, s, W, R, p1;
+    bool operator==(const Key& o) const { return d == o.d && s == o.s && W == o.W && R == o.R && p1 == o.p1; }
+};
+
+template <typename D, typename S>
+hipError_t launch_step(const Key& k, const StepBatch& b, int grid, hipStream_t st) {
+#define GEFEN_STEP_CASE(WW, RR)                                                                  \
+    if (k.W == WW && k.R == RR) {                                                               \
+        if (k.p1) hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, true>), dim3(grid), dim3(kThreads), 0, st, b); \
+        else hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false>), dim3(grid), dim3(kThreads), 0, st, b);     \
+        return hipGetLastError();                                                               \
+    }
+    if (k.R == 0) {
+        hipLaunchKernelGGL((k_gefen_step_long<D, S>), dim3(grid), dim3(kThreads), 0, st, b);
+        return hipGetLastError();
+    }
+    if (sizeof(D) == 2) {
+        GEFEN_STEP_CASE(8, 1) GEFEN_STEP_CASE(8, 2) GEFEN_STEP_CASE(8, 4) GEFEN_STEP_CASE(8, 8)
+        GEFEN_STEP_CASE(4, 1) GEFEN_STEP_CASE(4, 2) GEFEN_STEP_CASE(4, 4) GEFEN_STEP_CASE(4, 8)
+    } else {
+        GEFEN_STEP_CASE(4, 1) GEFEN_STEP_CASE(4, 2) GEFEN_STEP_CASE(4, 4) GEFEN_STEP_CASE(4, 8)
+    }
+    GEFEN_STEP_CASE(1, 1) GEFEN_STEP_CASE(1, 2) GEFEN_STEP_CASE(1, 4) GEFEN_STEP_CASE(1, 8)
+#undef GEFEN_STEP_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t dispatch_step(const Key& k, const StepBatch& b, int grid, hipStream_t st) {
+    if (k.d == GEFEN_F32) return launch_step<float, float>(k, b, grid, st);
+    if (k.d == GEFEN_BF16 && k.s == GEFEN_BF16) return launch_step<bf16_t, bf16_t>(k, b, grid, st);
+    if (k.d == GEFEN_F16 && k.s == GEFEN_F16) return launch_step<f16_t, f16_t>(k, b, grid, st);
+    if (k.d == GEFEN_BF16 && k.s == GEFEN_F32) return launch_step<bf16_t, float>(k, b, grid, st);
+    if (k.d == GEFEN_F16 && k.s == GEFEN_F32) return launch_step<f16_t, float>(k, b, grid, st);
+    return hipErrorInvalidValue;
+}
+
+template <typename D, typename S>
+hipError_t launch_muon(const Key& k, const MuonBatch& b, int grid, hipStream_t st) {
+#define GEFEN_MUON_CASE(WW, RR)                                                                      \
+    if (k.W == WW && k.R == RR) {                                                                   \
+        hipLaunchKernelGGL((k_muon<D, S, WW, RR>), dim3(grid), dim3(kThreads), 0, st, b);           \
+        return hipGetLastError();                                                                   \
+    }
+    if (k.R == 0) {
+        hipLaunchKernelGGL((k_muon_long<D, S>), dim3(grid), dim3(kThreads), 0, st, b);
+        return hipGetLastError();
+    }
+    if (sizeof(D) == 2) {
+        GEFEN_MUON_CASE(8, 1) GEFEN_MUON_CASE(8, 2) GEFEN_MUON_CASE(8, 4) GEFEN_MUON_CASE(8, 8)
+        GEFEN_MUON_CASE(4, 1) GEFEN_MUON_CASE(4, 2) GEFEN_MUON_CASE(4, 4) GEFEN_MUON_CASE(4, 8)
+    } else {
+        GEFEN_MUON_CASE(4, 1) GEFEN_MUON_CASE(4, 2) GEFEN_MUON_CASE(4, 4) GEFEN_MUON_CASE(4, 8)
+    }
+    GEFEN_MUON_CASE(1, 1) GEFEN_MUON_CASE(1, 2) GEFEN_MUON_CASE(1, 4) GEFEN_MUON_CASE(1, 8)
+#undef GEFEN_MUON_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t dispatch_muon(const Key& k, const MuonBatch& b, int grid, hipStream_t st) {
+    if (k.d == GEFEN_F32) return launch_muon<float, float>(k, b, grid, st);
+    if (k.d == GEFEN_BF16 && k.s == GEFEN_BF16) return launch_muon<bf16_t, bf16_t>(k, b, grid, st);
+    if (k.d == GEFEN_F16 && k.s == GEFEN_F16) return launch_muon<f16_t, f16_t>(k, b, grid, st);
+    if (k.d == GEFEN_BF16 && k.s == GEFEN_F32) return launch_muon<bf16_t, float>(k, b, grid, st);
+    if (k.d == GEFEN_F16 && k.s == GEFEN_F32) return launch_muon<f16_t, float>(k, b, grid, st);
+    return hipErrorInvalidValue;
+}
+
+bool valid_pair(int d, int s) { return valid_dtype(d) && valid_dtype(s) && (d == s || s == GEFEN_F32); }
+
+// Work of one task in workgroups for its kernel key.
+int32_t task_wgs(const Key& k, int64_t nrows, int lpr_log2) {
+    if (k.R == 0) return (int32_t)nrows;
+    const int64_t rpw = 64 >> lpr_log2;
+    const int64_t units = (nrows + rpw - 1) / rpw;
+    return (int32_t)((units + 4 * kIter - 1) / (4 * kIter));
+}
+
+struct PendingStep {
+    Key key;
+    StepTask task;
+};
+
+int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st) {
+    // group by kernel key, launch up to kMaxBatch tasks per launch
+    std::vector<bool> done(pend.size(), false);
+    for (size_t i = 0; i < pend.size(); ++i) {
+        if (done[i]) continue;
+        StepBatch b;
+        memset(&b, 0, sizeof(b));
+        b.tables = tables;
+        int n = 0;
+        int64_t wg = 0;
+        for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
+            if (done[j] || !(pend[j].key == pend[i].key)) continue;
+            if (wg + pend[j].task.nwg > INT32_MAX) break;
+            b.t[n] = pend[j].task;
+            b.wg_begin[n] = (int32_t)wg;
+            wg += pend[j].task.nwg;
+            ++n;
+            done[j] = true;
+        }
+        b.wg_begin[n] = (int32_t)wg;
+        b.ntasks = n;
+        if (wg == 0) continue;
+        hipError_t e = dispatch_step(pend[i].key, b, (int)wg, st);
+        if (e != hipSuccess) return hip_status(e, "gefen step launch");
+    }
+    return GEFEN_OK;
+}
+
+// Build the StepTask of one tensor.  mode / stepsize select the stepsize source.
+int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, PendingStep& out) {
+    const int64_t n = in.numel;
+    const int64_t P = in.period;
+    if (P <= 0 || n % P) return fail_inval("period %lld does not divide numel %lld", (long long)P, (long long)n);
+    // period-one mode (per-element vmean, magnitude per divisor block) is the fused
+    // step of a P = 1 tensor; the stepsize / given-vmean entry points use rows of P
+    const bool p1 = (P == 1 && mode == kVmeanUpdate);
+    const int64_t rowlen = p1 ? in.period_one_divisor : P;
+    if (rowlen <= 0 || n % rowlen) return fail_inval("magnitude block %lld does not divide numel %lld",
+                                                     (long long)rowlen, (long long)n);
+    if (p1 && rowlen > 256 * 64) return fail_inval("period_one_divisor %lld is too large", (long long)rowlen);
+    if (P > INT32_MAX) return fail_inval("period %lld is too large", (long long)P);
+    const int dsz = dtype_size(in.param_dtype), ssz = dtype_size(in.state_dtype);
+    const int W = pick_width(dsz, rowlen, {in.p, in.grad}, 1, in.m_codebook, ssz, p1 ? in.vmean : nullptr);
+    const int64_t nvec = rowlen / W;
+    const int l2 = lpr_log2_for(nvec);
+    int R = r_bucket(nvec, l2);
+    if (p1 && R == 0) return fail_inval("period_one_divisor %lld is too large", (long long)rowlen);
+    Key k{in.param_dtype, in.state_dtype, R == 0 ? 1 : W, R, p1 ? 1 : 0};
+    StepTask& t = out.task;
+    memset(&t, 0, sizeof(t));
+    t.p = in.p;
+    t.g = in.grad;
+    t.idx = in.m_codebook;
+    t.mag = in.m_magnitude;
+    t.vmean = in.vmean;
+    t.stepsize = stepsize;
+    t.nrows = n / rowlen;
+    t.rowlen = rowlen;
+    t.period = (int32_t)(p1 ? 1 : P);
+    t.nvec = (int32_t)std::min<int64_t>(nvec, INT32_MAX);
+    t.lpr_log2 = l2;
+    t.mode = mode;
+    t.b1c = (float)(1.0 - in.beta1);
+    t.b2 = (float)in.beta2;
+    t.omb2 = (float)(1.0 - in.beta2);
+    t.sqrt_bc2 = (float)sqrt(in.bias_correction_2);
+    t.eps = (float)in.eps;
+    t.inv_bc1 = (float)(1.0 / in.bias_correction_1);
+    t.lr = (float)in.lr;
+    t.do_wd = in.weight_decay > 0.0;
+    t.wdf = (float)(1.0 - in.lr * in.weight_decay);
+    t.nwg = task_wgs(k, t.nrows, l2);
+    out.key = k;
+    return GEFEN_OK;
+}
+
+int check_step_task(const gefen_step_task& t) {
+    if (t.numel < 0) return fail_inval("numel must be non-negative");
+    if (!valid_pair(t.param_dtype, t.state_dtype))
+        return fail_inval("unsupported dtype pair (param %d, state %d)", t.param_dtype, t.state_dtype);
+    if (t.numel == 0) return GEFEN_OK;
+    if (!t.p || !t.grad || !t.m_codebook || !t.m_magnitude || !t.vmean)
+        return fail_inval("null tensor pointer");
+    if (!(t.bias_correction_1 > 0.0)) return fail_inval("Expected bias_correction_1 to be positive, got %g", t.bias_correction_1);
+    if (!(t.bias_correction_2 > 0.0)) return fail_inval("Expected bias_correction_2 to be positive, got %g", t.bias_correction_2);
+    if (t.eps < 0.0) return fail_inval("Expected eps to be non-negative, got %g", t.eps);
+    return GEFEN_OK;
+}
+
+int check_codebook(const float* cb, int K) {
+    if (!cb) return fail_inval("null codebook");
+    if (K <= 0 || K > 256) return fail_inval("Expected codebook to have at most 256 entries, got %d", K);
+    return GEFEN_OK;
+}
+
+// Temporary codebook tables for the single-call entry points.
+struct TempTables {
+    void* ptr = nullptr;
+    hipStream_t st = nullptr;
+    int init(const float* cb, int K, hipStream_t s) {
+        st = s;
+        hipError_t e = hipMallocAsync(&ptr, sizeof(CodebookTables), s);
+        if (e != hipSuccess) return hip_status(e, "hipMallocAsync(codebook tables)");
+        return gefen_prepare_codebook(cb, K, ptr, reinterpret_cast<gefen_stream_t>(s));
+    }
+    ~TempTables() {
+        if (ptr) (void)hipFreeAsync(ptr, st);
+    }
+};
+
+}  // namespace
+}  // namespace gefen
+
+using namespace gefen;
+
+extern "C" int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const void* tables,
+                                gefen_stream_t stream) {
+    if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
+    if (!tables) return fail_inval("null codebook tables");
+    std::vector<PendingStep> pend;
+    pend.reserve(ntasks);
+    for (int i = 0; i < ntasks; ++i) {
+        int rc = check_step_task(tasks[i]);
+        if (rc) return rc;
+        if (tasks[i].numel == 0) continue;
+        PendingStep ps;
+        rc = make_step_task(tasks[i], kVmeanUpdate, nullptr, ps);
+        if (rc) return rc;
+        pend.push_back(ps);
+    }
+    return flush_steps(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
+}
+
+static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign, void* mag,
+                         int mag_dtype, void* vmean, int vmean_dtype, const float* stepsize,
+                         const float* codebook, int K, int packed, int64_t num_blocks, int64_t period,
+                         int64_t pod, int mode, double beta1, double beta2, double lr, double bc1,
+                         double bc2, double eps, gefen_stream_t stream) {
+    if (packed) return fail_inval("packed 4-bit codebook indices are not supported");
+    int rc = check_codebook(codebook, K);
+    if (rc) return rc;
+    if (!valid_dtype(param_dtype)) return fail_inval("unsupported parameter dtype %d", param_dtype);
+    if (!valid_pair(param_dtype, mag_dtype))
+        return fail_inval("Expected m_magnitude to be float32, float16, or bfloat16 matching the parameters");
+    if (mode != kStepsizeGiven && vmean_dtype != mag_dtype)
+        return fail_inval("vmean dtype %d must match m_magnitude dtype %d", vmean_dtype, mag_dtype);
+    if (num_blocks < 0 || period <= 0) return fail_inval("Expected a positive period, got %lld", (long long)period);
+    gefen_step_task t;
+    memset(&t, 0, sizeof(t));
+    t.p = p;
+    t.grad = grad;
+    t.m_codebook = m_sign;
+    t.m_magnitude = mag;
+    t.vmean = mode == kStepsizeGiven ? (void*)stepsize : vmean;
+    t.numel = num_blocks * period;
+    t.period = period;
+    t.period_one_divisor = pod;
+    t.param_dtype = param_dtype;
+    t.state_dtype = mag_dtype;
+    t.beta1 = beta1;
+    t.beta2 = beta2;
+    t.lr = lr;
+    t.eps = eps;
+    t.weight_decay = 0.0;
+    t.bias_correction_1 = bc1;
+    t.bias_correction_2 = bc2;
+    rc = check_step_task(t);
+    if (rc) return rc;
+    if (t.numel == 0) return GEFEN_OK;
+    PendingStep ps;
+    rc = make_step_task(t, mode, stepsize, ps);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    TempTables tt;
+    rc = tt.init(codebook, K, st);
+    if (rc) return rc;
+    std::vector<PendingStep> pend(1, ps);
+    return flush_steps(pend, static_cast<const CodebookTables*>(tt.ptr), st);
+}
+
+extern "C" int gefen_automatic_fused_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,
+                                            void* m_magnitude, int magnitude_dtype, const float* stepsize,
+                                            const float* codebook, int codebook_size, int packed_indices,
+                                            int64_t num_blocks, int64_t period, double beta1, double lr,
+                                            gefen_stream_t stream) {
+    if (!stepsize && num_blocks > 0) return fail_inval("null stepsize");
+    return single_update(p, grad, param_dtype, m_sign, m_magnitude, magnitude_dtype, nullptr,
+                         magnitude_dtype, stepsize, codebook, codebook_size, packed_indices,
+                         num_blocks, period, 0, kStepsizeGiven, beta1, 0.0, lr, 1.0, 1.0, 0.0, stream);
+}
+
+extern "C" int gefen_automatic_fused_update_from_vmean(
+    void* p, const void* grad, int param_dtype, uint8_t* m_sign, void* m_magnitude, int magnitude_dtype,
+    const void* vmean, int vmean_dtype, const float* codebook, int codebook_size, int packed_indices,
+    int64_t num_blocks, int64_t period, double beta1, double lr, double bias_correction_1,
+    double bias_correction_2, double eps, gefen_stream_t stream) {
+    return single_update(p, grad, param_dtype, m_sign, m_magnitude, magnitude_dtype,
+                         const_cast<void*>(vmean), vmean_dtype, nullptr, codebook, codebook_size,
+                         packed_indices, num_blocks, period, 0, kVmeanGiven, beta1, 0.0, lr,
+                         bias_correction_1, bias_correction_2, eps, stream);
+}
+
+extern "C" int gefen_automatic_period1_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,
+                                              void* m_magnitude, int magnitude_dtype, void* vmean,
+                                              int vmean_dtype, const float* codebook, int codebook_size,
+                                              int64_t numel, int64_t period_one_divisor, double beta1,
+                                              double beta2, double lr, double bias_correction_1,
+                                              double bias_correction_2, double eps, gefen_stream_t stream) {
+    if (period_one_divisor <= 0) return fail_inval("Expected period_one_divisor to be positive, got %lld",
+                                                   (long long)period_one_divisor);
+    if (!(beta2 >= 0.0 && beta2 <= 1.0)) return fail_inval("Expected beta2 to be in [0, 1], got %g", beta2);
+    return single_update(p, grad, param_dtype, m_sign, m_magnitude, magnitude_dtype, vmean, vmean_dtype,
+                         nullptr, codebook, codebook_size, 0, numel, 1, period_one_divisor, kVmeanUpdate,
+                         beta1, beta2, lr, bias_correction_1, bias_correction_2, eps, stream);
+}
+
+// ------------------------------------------------------------------------- muon
+namespace gefen {
+namespace {
+struct PendingMuon {
+    Key key;
+    MuonTask task;
+};
+
+int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
+    const int64_t n = in.numel, rowlen = in.block;
+    if (rowlen <= 0 || n % rowlen) return fail_inval("block %lld does not divide numel %lld",
+                                                     (long long)rowlen, (long long)n);
+    if (!valid_pair(in.grad_dtype, in.state_dtype))
+        return fail_inval("unsupported dtype pair (grad %d, state %d)", in.grad_dtype, in.state_dtype);
+    if (!(in.momentum >= 0.0 && in.momentum < 1.0))
+        return fail_inval("Expected beta1 to be in [0, 1), got %g", in.momentum);
+    if (n > 0 && (!in.grad || !in.m_codebook || !in.m_magnitude || !in.out)) return fail_inval("null tensor pointer");
+    const int dsz = dtype_size(in.grad_dtype);
+    const int W = pick_width(dsz, rowlen, {in.grad, in.out}, 1, in.m_codebook, 0, nullptr);
+    const int64_t nvec = rowlen / W;
+    const int l2 = lpr_log2_for(nvec);
+    const int R = r_bucket(nvec, l2);
+    Key k{in.grad_dtype, in.state_dtype, R == 0 ? 1 : W, R, 0};
+    MuonTask& t = out.task;
+    memset(&t, 0, sizeof(t));
+    t.g = in.grad;
+    t.idx = in.m_codebook;
+    t.mag = in.m_magnitude;
+    t.out = in.out;
+    t.nrows = n / rowlen;
+    t.rowlen = rowlen;
+    t.nvec = (int32_t)std::min<int64_t>(nvec, INT32_MAX);
+    t.lpr_log2 = l2;
+    t.w = (float)(1.0 - in.momentum);
+    t.mom = (float)in.momentum;
+    float alpha = (float)(1.0 - in.momentum);
+    float tiny = in.grad_dtype == GEFEN_F16 ? 6.103515625e-05f : 1.17549435e-38f;
+    // reduced-dtype add_(alpha=) rounds alpha to the tensor dtype; tiny lives in the state dtype
+    auto round_host = [](float v, int dt) -> float {
+        if (dt == GEFEN_F32) return v;
+        if (dt == GEFEN_BF16) {
+            uint32_t u;
+            memcpy(&u, &v, 4);
+            u += 0x7fffu + ((u >> 16) & 1u);
+            u &= 0xffff0000u;
+            float r;
+            memcpy(&r, &u, 4);
+            return r;
+        }
+        _Float16 h = (_Float16)v;
+        return (float)h;
+    };
+    t.alpha = round_host(alpha, in.grad_dtype);
+    t.tiny = round_host(tiny, in.state_dtype);
+    t.nesterov = in.nesterov ? 1 : 0;
+    t.nwg = task_wgs(k, t.nrows, l2);
+    out.key = k;
+    return GEFEN_OK;
+}
+
+int flush_muon(std::vector<PendingMuon>& pend, const CodebookTables* tables, hipStream_t st) {
+    std::vector<bool> done(pend.size(), false);
+    for (size_t i = 0; i < pend.size(); ++i) {
+        if (done[i]) continue;
+        MuonBatch b;
+        memset(&b, 0, sizeof(b));
+        b.tables = tables;
+        int n = 0;
+        int64_t wg = 0;
+        for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
+            if (done[j] || !(pend[j].key == pend[i].key)) continue;
+            if (wg + pend[j].task.nwg > INT32_MAX) break;
+            b.t[n] = pend[j].task;
+            b.wg_begin[n] = (int32_t)wg;
+            wg += pend[j].task.nwg;
+            ++n;
+            done[j] = true;
+        }
+        b.wg_begin[n] = (int32_t)wg;
+        b.ntasks = n;
+        if (wg == 0) continue;
+        hipError_t e = dispatch_muon(pend[i].key, b, (int)wg, st);
+        if (e != hipSuccess) return hip_status(e, "gefen muon launch");
+    }
+    return GEFEN_OK;
+}
+}  // namespace
+}  // namespace gefen
+
+extern "C" int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* tables,
+                                gefen_stream_t stream) {
+    if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
+    if (!tables) return fail_inval("null codebook tables");
+    std::vector<PendingMuon> pend;
+    for (int i = 0; i < ntasks; ++i) {
+        if (tasks[i].numel == 0) continue;
+        PendingMuon pm;
+        int rc = make_muon_task(tasks[i], pm);
+        if (rc) return rc;
+        pend.push_back(pm);
+    }
+    return flush_muon(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int gefen_automatic_muon_momentum(const void* grad, int grad_dtype, uint8_t* m_sign,
+                                             void* m_magnitude, int magnitude_dtype, const float* codebook,
+                                             int codebook_size, void* momentum_update, int packed_indices,
+                                             int64_t num_blocks, int64_t period, double beta1,
+                                             gefen_stream_t stream) {
+    if (packed_indices) return fail_inval("packed 4-bit codebook indices are not supported");
+    int rc = check_codebook(codebook, codebook_size);
+    if (rc) return rc;
+    if (num_blocks < 0 || period <= 0) return fail_inval("Expected a positive period, got %lld", (long long)period);
+    gefen_muon_task t;
+    memset(&t, 0, sizeof(t));
+    t.grad = grad;
+    t.m_codebook = m_sign;
+    t.m_magnitude = m_magnitude;
+    t.out = momentum_update;
+    t.numel = num_blocks * period;
+    t.block = period;
+    t.grad_dtype = grad_dtype;
+    t.state_dtype = magnitude_dtype;
+    t.momentum = beta1;
+    t.nesterov = 0;
+    if (t.numel == 0) return GEFEN_OK;
+    PendingMuon pm;
+    rc = make_muon_task(t, pm);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    TempTables tt;
+    rc = tt.init(codebook, codebook_size, st);
+    if (rc) return rc;
+    std::vector<PendingMuon> pend(1, pm);
+    return flush_muon(pend, static_cast<const CodebookTables*>(tt.ptr), st);
+}
+
+extern "C" int gefen_automatic_vmean_update(void* vmean, int vmean_dtype, const void* grad, int grad_dtype,
+                                            int64_t num_blocks, int64_t period, double beta2,
+                                            gefen_stream_t stream) {
+    if (!valid_dtype(vmean_dtype))
+        return fail_inval("Expected vmean to be float32, float16, or bfloat16, got %d", vmean_dtype);
+    if (!valid_dtype(grad_dtype)) return fail_inval("unsupported grad dtype %d", grad_dtype);
+    if (!(beta2 >= 0.0 && beta2 <= 1.0)) return fail_inval("Expected beta2 to be in [0, 1], got %g", beta2);
+    if (num_blocks < 0 || period <= 0) return fail_inval("Expected a positive period, got %lld", (long long)period);
+    if (num_blocks == 0) return GEFEN_OK;
+    if (!vmean || !grad) return fail_inval("null tensor pointer");
+    const int l2 = lpr_log2_for(period);
+    const int64_t rpw = 64 >> l2;
+    const int64_t units = (num_blocks + rpw - 1) / rpw;
+    const int64_t grid = (units + 3) / 4;
+    if (grid > INT32_MAX) return fail_inval("tensor too large");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const float b2 = (float)beta2, omb2 = (float)(1.0 - beta2);
+#define GEFEN_VMEAN(G, S)                                                                               \
+    hipLaunchKernelGGL((k_vmean<G, S>), dim3((unsigned)grid), dim3(kThreads), 0, st, static_cast<S*>(vmean), \
+                       static_cast<const G*>(grad), num_blocks, period, l2, b2, omb2)
+    auto launch_s = [&](auto gtag) {
+        using G = decltype(gtag);
+        if (vmean_dtype == GEFEN_F32) GEFEN_VMEAN(G, float);
+        else if (vmean_dtype == GEFEN_BF16) GEFEN_VMEAN(G, bf16_t);
+        else GEFEN_VMEAN(G, f16_t);
+    };
+    if (grad_dtype == GEFEN_F32) launch_s(float{});
+    else if (grad_dtype == GEFEN_BF16) launch_s(bf16_t{});
+    else launch_s(f16_t{});
+#undef GEFEN_VMEAN
+    return launch_status("gefen vmean launch");
+}

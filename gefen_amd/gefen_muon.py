@@ -1,0 +1,220 @@
+"""GefenMuon on MI355X (reference: gefen_muon.py, ndvbd/Gefen 1.2.3).
+
+Muon with Gefen's 8-bit quantised momentum.  Per step, one batched HIP launch
+updates the quantised momentum of every tensor and writes the Nesterov blend
+(gefen_muon.py:302-316, CPU-path rounding); Newton-Schulz orthogonalisation
+(gefen_muon.py:16-51) runs on the device; the parameter update follows the
+reference's CPU arithmetic (gefen_muon.py:325-329).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Iterable, Optional, Tuple, Union
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from gefen_amd import _lib
+from gefen_amd.gefen import Gefen, _DTYPE_CODE, automatic_partition_view
+
+EPS = 1e-7
+DEFAULT_A = 3.4445
+DEFAULT_B = -4.7750
+DEFAULT_C = 2.0315
+DEFAULT_NS_STEPS = 5
+
+
+def _zeropower_via_newtonschulz(grad: torch.Tensor, ns_coefficients: Tuple[float, float, float], ns_steps: int,
+                                eps: float) -> torch.Tensor:
+    """Quintic Newton-Schulz iteration in bf16 (gefen_muon.py:16-51)."""
+    if ns_steps >= 100:
+        raise ValueError("Number of steps must be less than 100 for computational efficiency")
+    if len(grad.shape) != 2:
+        raise ValueError("Input tensor gradient must be a 2D matrix")
+    if len(ns_coefficients) != 3:
+        raise ValueError("Coefficients must be a tuple of exactly 3 values")
+    from gefen_amd.newton_schulz import newton_schulz_bf16
+
+    return newton_schulz_bf16(grad, ns_coefficients, ns_steps, eps)
+
+
+def _adjust_lr(lr: float, adjust_lr_fn: Optional[str], param_shape: torch.Size) -> float:
+    """gefen_muon.py:54-67."""
+    if isinstance(lr, torch.Tensor):
+        lr = lr.item()
+    rows, cols = param_shape[:2]
+    if adjust_lr_fn is None or adjust_lr_fn == "original":
+        ratio = math.sqrt(max(1, rows / cols))
+    elif adjust_lr_fn == "match_rms_adamw":
+        ratio = 0.2 * math.sqrt(max(rows, cols))
+    else:
+        ratio = 1.0
+    return lr * ratio
+
+
+def _apply_update(p: torch.Tensor, update: torch.Tensor, lr: float, weight_decay: float, adjusted_lr: float,
+                  transposed: bool) -> None:
+    """p.mul_(1 - lr*wd); p.add_(update, alpha=-adjusted_lr) with the reference's
+    CPU rounding (gefen_muon.py:325-329): reduced dtypes round alpha to the
+    dtype, and the element-wise path of a transposed update also rounds the
+    product; fp32 is one fused multiply-add."""
+    if weight_decay > 0.0:
+        p.mul_(1 - lr * weight_decay)
+    if p.dtype == torch.float32:
+        p.add_(update.float(), alpha=-adjusted_lr)
+        return
+    alpha = torch.tensor(-adjusted_lr, dtype=torch.float32).to(p.dtype).float().item()
+    prod = update.float() * alpha
+    if transposed:
+        prod = prod.to(p.dtype).float()
+    p.copy_((p.float() + prod).to(p.dtype))
+
+
+class GefenMuon(Gefen):
+    """GefenMuon (gefen_muon.py:70-350)."""
+
+    def __init__(self, params: Iterable[Union[nn.Parameter, Tuple[str, nn.Parameter]]],
+                 lr: Union[float, torch.Tensor] = 1e-3, weight_decay: float = 0.1, momentum: float = 0.95,
+                 nesterov: bool = True,
+                 ns_coefficients: Tuple[float, float, float] = (DEFAULT_A, DEFAULT_B, DEFAULT_C), eps: float = EPS,
+                 ns_steps: int = DEFAULT_NS_STEPS, adjust_lr_fn: Optional[str] = None, *, fused: bool = True,
+                 verbose: bool = False) -> None:
+        if isinstance(lr, torch.Tensor) and lr.numel() != 1:
+            raise ValueError("Tensor lr must be 1-element")
+        if not 0.0 <= lr:
+            raise ValueError("Learning rate should be >= 0 but is: {}".format(lr))
+        if not 0.0 <= momentum:
+            raise ValueError("momentum should be >= 0 but is: {}".format(momentum))
+        if not 0.0 <= weight_decay:
+            raise ValueError("weight decay should be >= 0 but is: {}".format(weight_decay))
+        if adjust_lr_fn is not None and adjust_lr_fn not in ["original", "match_rms_adamw"]:
+            raise ValueError("Adjust learning rate function {} is not supported".format(adjust_lr_fn))
+        super().__init__(params, lr=lr, betas=(momentum, 0.0), eps=eps, weight_decay=weight_decay, fused=fused,
+                         verbose=verbose)
+        for group in self.param_groups:
+            group["momentum"] = momentum
+            group["nesterov"] = nesterov
+            group["ns_coefficients"] = ns_coefficients
+            group["ns_steps"] = ns_steps
+            group["adjust_lr_fn"] = adjust_lr_fn
+            for p in group["params"]:
+                if p.ndim != 2:
+                    raise ValueError("GefenMuon only supports 2D parameters whereas we found a parameter with size: "
+                                     "{}".format(p.size()))
+
+    def _init_gefen_muon_state(self, state, grad_view: torch.Tensor) -> None:
+        self._init_gefen_state(state, grad_view)
+
+    def _init_states(self, pending) -> None:
+        need = [(p, grad) for (group, p, local_p, grad) in pending
+                if "automatic_period" not in self.state[p] and grad.numel() > 1]
+        periods = self._predict_periods(need) if need else []
+        for (p, _), period in zip(need, periods):
+            self.state[p]["automatic_period"] = period
+        for group, p, local_p, grad in pending:
+            st = self.state[p]
+            n = grad.numel()
+            if "automatic_period" not in st:
+                st["automatic_period"] = 1
+            period = st["automatic_period"]
+            if n % period != 0:
+                raise ValueError("Automatic partition period {} does not divide local shard of parameter {} with "
+                                 "numel {}".format(period, group["name"], n))
+            st["step"] = 0
+            self._init_gefen_muon_state(st, automatic_partition_view(grad.reshape(-1), period))
+            self._print_period(group["name"], local_p, period)
+
+    def _step_all(self) -> None:
+        items = []
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                name = group["name"]
+                local_p = self._resolve_local_tensor(p, "parameter {}".format(name))
+                grad = self._resolve_local_tensor(p.grad, "gradient {}".format(name))
+                if torch.is_complex(local_p):
+                    raise RuntimeError("GefenMuon does not support complex parameters")
+                if grad.is_sparse:
+                    raise RuntimeError("GefenMuon does not support sparse gradients")
+                if grad.ndim != 2:
+                    raise ValueError("GefenMuon gradient must be a 2D matrix for {}".format(name))
+                if local_p.numel() != grad.numel():
+                    raise ValueError("Local parameter shard numel {} does not match local gradient numel {} for {}."
+                                     .format(local_p.numel(), grad.numel(), name))
+                if grad.numel() == 0:
+                    continue
+                if grad.device.type != "cuda":
+                    raise RuntimeError("gefen_amd runs on HIP devices; {} is on {}".format(name, grad.device))
+                items.append((group, p, local_p, grad))
+        if not items:
+            return
+        fresh = [it for it in items if "step" not in self.state[it[1]]]
+        if fresh:
+            self._init_states(fresh)
+        if self._gefen_codebook is None:
+            raise ValueError("Expected Gefen codebook to be initialized before fused GefenMuon update.")
+        tables = self._codebook_tables()
+        tasks = np.zeros(len(items), dtype=_lib.MUON_TASK)
+        outs = []
+        keep = []
+        for i, (group, p, local_p, grad) in enumerate(items):
+            st = self.state[p]
+            period = st["automatic_period"]
+            flat = grad.reshape(-1)
+            if not flat.is_contiguous():
+                flat = flat.contiguous()
+            keep.append(flat)
+            out = torch.empty_like(flat)
+            outs.append(out)
+            t = tasks[i]
+            t["grad"] = flat.data_ptr()
+            t["m_codebook"] = st["m_codebook"].data_ptr()
+            t["m_magnitude"] = st["m_magnitude"].data_ptr()
+            t["out"] = out.data_ptr()
+            t["numel"] = flat.numel()
+            t["block"] = self._period_one_divisor_from_state(st, flat.numel()) if period == 1 else period
+            t["grad_dtype"] = _DTYPE_CODE[flat.dtype]
+            t["state_dtype"] = _DTYPE_CODE[st["m_magnitude"].dtype]
+            t["momentum"] = group["momentum"]
+            t["nesterov"] = 1 if group["nesterov"] else 0
+        dev = items[0][3].device
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            rc = lib.gefen_muon_tasks(tasks.ctypes.data, len(items), tables.data_ptr(),
+                                      torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(rc, "gefen_muon_tasks")
+        for (group, p, local_p, grad), out in zip(items, outs):
+            st = self.state[p]
+            st["step"] += 1
+            update = _zeropower_via_newtonschulz(out.view_as(grad), group["ns_coefficients"], group["ns_steps"],
+                                                 group["eps"])
+            lr = group["lr"]
+            lr = float(lr.item()) if torch.is_tensor(lr) else float(lr)
+            adjusted = _adjust_lr(lr, group["adjust_lr_fn"], p.shape)
+            if local_p.is_contiguous():
+                target = local_p
+            elif hasattr(p, "to_local") and hasattr(p, "placements"):
+                target = local_p.contiguous()
+            else:
+                raise ValueError("GefenMuon fused update requires a contiguous parameter tensor for {}.".format(
+                    group["name"]))
+            _apply_update(target, update, lr, group["weight_decay"], adjusted, grad.size(0) > grad.size(1))
+            if target is not local_p:
+                local_p.copy_(target)
+        del keep
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        """gefen_muon.py:331-350: closure first, then the codebook refresh."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self._maybe_refresh_gefen_codebook()
+        self._maybe_save_gefen_grad_histogram()
+        self._step_all()
+        self._gefen_global_step += 1
+        return loss

@@ -121,3 +121,51 @@ def checksum(arr: np.ndarray) -> int:
     with np.errstate(over="ignore"):
         h = splitmix64(w ^ (np.arange(w.size, dtype=np.uint64) * GAMMA))
         return int(np.bitwise_xor.reduce(h)) if h.size else 0
+
+
+# --------------------------------------------------------------------------- device twin
+_SYNTH = None
+
+
+def _synth_lib():
+    global _SYNTH
+    if _SYNTH is None:
+        import ctypes
+        import os
+        from pathlib import Path
+
+        path = Path(__file__).resolve().parent / "libgefen_synth.so"
+        if not path.exists():
+            raise ImportError("{} is missing; build it with `python -m gefen_amd.build`".format(path))
+        lib = ctypes.CDLL(str(path), mode=os.RTLD_LOCAL)
+        lib.gefen_synth_fill.restype = ctypes.c_int
+        lib.gefen_synth_fill.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_double, ctypes.c_void_p]
+        lib.gefen_last_error.restype = ctypes.c_char_p
+        _SYNTH = lib
+    return _SYNTH
+
+
+KIND_ROW_SCALED, KIND_NORMAL, KIND_STUDENT_T3 = 0, 1, 2
+
+
+def fill_device(t, seed: int, stream: int, kind: int, cols: int = 0, e_lo: int = 0, e_hi: int = 0,
+                mult: float = 1.0) -> None:
+    """Fill a contiguous HIP tensor with the values numpy would produce:
+    kind 0 = row_scaled_normal(seed, stream, numel//cols, cols, e_lo, e_hi),
+    kind 1 = normal(make_key(seed, stream), numel) * mult,
+    kind 2 = student_t3(make_key(seed, stream), numel) * mult."""
+    import torch
+
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[t.dtype]
+    if not t.is_contiguous():
+        raise ValueError("fill_device needs a contiguous tensor")
+    n = t.numel()
+    cols = cols or max(n, 1)
+    with torch.cuda.device(t.device):
+        rc = _synth_lib().gefen_synth_fill(t.data_ptr(), code, n, cols, seed & 0xFFFFFFFFFFFFFFFF,
+                                           stream & 0xFFFFFFFFFFFFFFFF, e_lo, e_hi, kind, float(mult),
+                                           torch.cuda.current_stream(t.device).cuda_stream)
+    if rc:
+        raise RuntimeError(_synth_lib().gefen_last_error().decode())

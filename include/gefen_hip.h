@@ -1,0 +1,208 @@
+/*
+ * gefen_hip.h -- C ABI of the MI355X-native Gefen optimizer step.
+ *
+ * Every entry point takes raw device pointers, element counts, dtype codes and
+ * scalars as double, launches asynchronously on `stream` (a hipStream_t; 0 is
+ * the null stream) and returns
+ *   GEFEN_OK (0), GEFEN_EINVAL (1: invalid argument, ValueError in Python),
+ *   GEFEN_ERUNTIME (2: HIP or runtime failure, RuntimeError in Python).
+ * gefen_last_error() returns the message of the calling thread's last failure.
+ *
+ * Numerics follow the reference's CPU path (fused=False) of ndvbd/Gefen 1.2.3,
+ * not its CUDA kernels: codebook indices, magnitudes and histogram counts are
+ * bit-identical to that path; parameters agree within the stated tolerances.
+ *
+ * The eleven functions of the reference's extension module
+ * (kernels/gefen_cuda_binding.cpp:107-217) each have one counterpart here;
+ * the comment above each names the reference interface it replaces.
+ */
+#ifndef GEFEN_HIP_H
+#define GEFEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* gefen_stream_t; /* == hipStream_t */
+
+enum { GEFEN_OK = 0, GEFEN_EINVAL = 1, GEFEN_ERUNTIME = 2 };
+/* element types of parameters, gradients and optimizer state */
+enum { GEFEN_F32 = 0, GEFEN_F16 = 1, GEFEN_BF16 = 2 };
+
+const char* gefen_last_error(void);
+int gefen_abi_version(void);
+/* sizeof(gefen_step_task) for which = 0, sizeof(gefen_muon_task) for which = 1:
+ * lets bindings check their mirror of the structs. */
+size_t gefen_struct_size(int which);
+
+/* ------------------------------------------------------------------ codebook tables
+ * Size in bytes of the prepared lookup tables of one codebook (sorted, <= 256
+ * entries); gefen_prepare_codebook fills them on `stream`.  Every update entry
+ * point that takes `tables` reads the codebook from them. */
+size_t gefen_codebook_tables_size(void);
+int gefen_prepare_codebook(const float* codebook, int codebook_size, void* tables,
+                           gefen_stream_t stream);
+
+/* ------------------------------------------------------------------ vmean
+ * Replaces automatic_vmean_update_cuda (kernels/automatic_vmean.py:10-55,
+ * automatic_vmean_kernel.cu:66-158).  vmean[r] = fma(mean_j f32(g[r,j])^2, 1-beta2,
+ * f32(vmean[r]) * beta2) rounded to vmean_dtype, as gefen.py:116-119. */
+int gefen_automatic_vmean_update(void* vmean, int vmean_dtype, const void* grad, int grad_dtype,
+                                 int64_t num_blocks, int64_t period, double beta2,
+                                 gefen_stream_t stream);
+
+/* ------------------------------------------------------------------ fused updates
+ * Replaces automatic_gefen_fused_update_cuda (automatic_gefen_fused.py:10-117,
+ * automatic_gefen_fused_kernel.cu:568-674): stepsize given per block (f32). */
+int gefen_automatic_fused_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,
+                                 void* m_magnitude, int magnitude_dtype, const float* stepsize,
+                                 const float* codebook, int codebook_size, int packed_indices,
+                                 int64_t num_blocks, int64_t period, double beta1, double lr,
+                                 gefen_stream_t stream);
+
+/* Replaces automatic_gefen_fused_update_from_vmean_cuda (automatic_gefen_fused.py:120-249,
+ * automatic_gefen_fused_kernel.cu:676-833): stepsize from the (already updated)
+ * vmean with gefen.py:1326-1327; momentum, quantisation and p update as
+ * gefen.py:1153-1206, 1328-1333. */
+int gefen_automatic_fused_update_from_vmean(void* p, const void* grad, int param_dtype,
+                                            uint8_t* m_sign, void* m_magnitude, int magnitude_dtype,
+                                            const void* vmean, int vmean_dtype,
+                                            const float* codebook, int codebook_size,
+                                            int packed_indices, int64_t num_blocks, int64_t period,
+                                            double beta1, double lr, double bias_correction_1,
+                                            double bias_correction_2, double eps,
+                                            gefen_stream_t stream);
+
+/* Replaces automatic_gefen_period1_update_cuda (automatic_gefen_fused.py:252-388,
+ * automatic_gefen_fused_kernel.cu:835-1000): per-element vmean and stepsize,
+ * one magnitude per block of period_one_divisor elements. */
+int gefen_automatic_period1_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,
+                                   void* m_magnitude, int magnitude_dtype, void* vmean,
+                                   int vmean_dtype, const float* codebook, int codebook_size,
+                                   int64_t numel, int64_t period_one_divisor, double beta1,
+                                   double beta2, double lr, double bias_correction_1,
+                                   double bias_correction_2, double eps, gefen_stream_t stream);
+
+/* Replaces automatic_gefen_muon_momentum_cuda (automatic_gefen_fused.py:391-489,
+ * automatic_gefen_fused_kernel.cu:1002-1103): quantised momentum EMA of
+ * gefen_muon.py:302-308 and 132-171 (every op rounded to the gradient dtype);
+ * writes the dequantised momentum into momentum_update. */
+int gefen_automatic_muon_momentum(const void* grad, int grad_dtype, uint8_t* m_sign,
+                                  void* m_magnitude, int magnitude_dtype, const float* codebook,
+                                  int codebook_size, void* momentum_update, int packed_indices,
+                                  int64_t num_blocks, int64_t period, double beta1,
+                                  gefen_stream_t stream);
+
+/* ------------------------------------------------------------------ whole step
+ * One tensor of Gefen._step_automatic (gefen.py:1270-1333) in one kernel pass:
+ * vmean EMA, weight decay, bias-corrected stepsize, momentum, quantisation and
+ * parameter update.  No reference counterpart as a single call: the reference
+ * issues vmean + update (+ a weight-decay pass) per tensor. */
+typedef struct gefen_step_task {
+    void* p;                    /* parameter, numel elements of param_dtype      */
+    const void* grad;           /* gradient, same dtype                          */
+    uint8_t* m_codebook;        /* codebook indices, numel bytes                 */
+    void* m_magnitude;          /* one per magnitude block, state_dtype          */
+    void* vmean;                /* one per period block (per element if P = 1)   */
+    int64_t numel;
+    int64_t period;             /* automatic period P (1 = period-one mode)      */
+    int64_t period_one_divisor; /* magnitude block for P = 1 (ignored if P > 1)  */
+    int32_t param_dtype;
+    int32_t state_dtype;
+    double beta1, beta2, lr, eps, weight_decay;
+    double bias_correction_1;   /* 1 - beta1**step, computed by the caller       */
+    double bias_correction_2;   /* 1 - beta2**step                               */
+} gefen_step_task;
+
+int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const void* tables,
+                     gefen_stream_t stream);
+
+/* GefenMuon momentum of many tensors with the Nesterov blend fused
+ * (gefen_muon.py:302-316): out = D(D(q*mu) + g*(1-mu)) if nesterov, else q. */
+typedef struct gefen_muon_task {
+    const void* grad;
+    uint8_t* m_codebook;
+    void* m_magnitude;
+    void* out;                  /* momentum update, numel elements of grad dtype */
+    int64_t numel;
+    int64_t block;              /* magnitude block length (P, or divisor if P=1) */
+    int32_t grad_dtype;
+    int32_t state_dtype;
+    double momentum;
+    int32_t nesterov;
+    int32_t pad;
+} gefen_muon_task;
+
+int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* tables,
+                     gefen_stream_t stream);
+
+/* ------------------------------------------------------------------ first step
+ * Replaces gefen_exact_histogram_cuda (exact_histogram_fused.py:10-58,
+ * exact_histogram_fused_kernel.cu:131-160): per block absmax normalisation,
+ * bin = clamp(floor((x + 1) / f32(2/bins)), 0, bins-1) as gefen.py:350-366;
+ * bin_counts (int64, bins <= 4096) is accumulated (+=). */
+int gefen_exact_histogram(const void* grad, int grad_dtype, int64_t numel, int64_t period,
+                          int64_t* bin_counts, int bins, gefen_stream_t stream);
+
+/* acc[b] = f32(acc[b] + f32(counts[b])): the fp32 host accumulation of
+ * gefen.py:331, 347 performed on the device. */
+int gefen_accumulate_counts(float* acc, const int64_t* counts, int bins, gefen_stream_t stream);
+
+/* Exact DP codebook (quantization.py:206-258, gefen.py:373-399) of a 4096-bin
+ * fp32 histogram, on the device.  workspace: gefen_exact_dp_workspace_size() bytes. */
+size_t gefen_exact_dp_workspace_size(int bins, int codebook_size);
+int gefen_exact_dp(const float* counts, int bins, int codebook_size, int force_endpoints,
+                   float* codebook_out, void* workspace, gefen_stream_t stream);
+
+/* Replaces average_adjacent_log_block_mean_difference_cuda (period_variance.py:127-161,
+ * period_variance_kernel.cu:320-396): out[0] = mean_j |m_{j+1} - m_j| of the
+ * block means of log(x + epsilon), out[1] = count of x + epsilon <= 0 (the
+ * caller raises when it is non-zero).  x = f64(f32(v)) if input_is_squared,
+ * else f64(f32(v))^2.  out: 2 doubles of device memory. */
+int gefen_average_adjacent_log_block_mean_difference(const void* values, int dtype, int64_t numel,
+                                                     int64_t period, int input_is_squared,
+                                                     double epsilon, double* out,
+                                                     gefen_stream_t stream);
+
+/* All period scores of one gradient at once (partitioning.py:119-167): for each
+ * divisor divs[d] (host array), scores[d] as above; scores[ndiv] = invalid count.
+ * mode 1 squares in fp32 first (Gefen._predict_period_from_grad_sq,
+ * gefen.py:812-813); mode 0 / 2 as input_is_squared true / false.
+ * workspace: gefen_period_scores_workspace_size() bytes. */
+size_t gefen_period_scores_workspace_size(int64_t numel, const int64_t* divs, int ndiv);
+int gefen_period_scores(const void* values, int dtype, int64_t numel, const int64_t* divs,
+                        int ndiv, int mode, double epsilon, double* scores, void* workspace,
+                        gefen_stream_t stream);
+
+/* Replace average_within_block_variance_cuda and
+ * average_within_block_coefficient_of_variation_cuda (period_variance.py:12-124,
+ * period_variance_kernel.cu:177-318).  out: variance -> out[0] = sqrt(mean of
+ * block variances); CoV -> out[0] = mean std/mean over blocks with a positive
+ * mean, out[1] = count of such blocks, out[2] = count of negative means. */
+int gefen_average_within_block_variance(const void* values, int dtype, int64_t numel,
+                                        int64_t period, int input_is_squared, double* out,
+                                        gefen_stream_t stream);
+int gefen_average_within_block_coefficient_of_variation(const void* values, int dtype,
+                                                        int64_t numel, int64_t period,
+                                                        int input_is_squared, double* out,
+                                                        gefen_stream_t stream);
+
+/* Replace gefen_lloyd_accumulate_cuda and gefen_lloyd_mse_cuda (lloyd_max_fused.py:10-143,
+ * lloyd_max_fused_kernel.cu:244-356): block absmax normalisation, nearest
+ * codeword; sums (f32) / counts (int64) and the two squared-error sums (f32)
+ * are accumulated (+=). */
+int gefen_lloyd_accumulate(const void* grad, int grad_dtype, int64_t numel, int64_t period,
+                           const float* codebook, int codebook_size, float* sums, int64_t* counts,
+                           gefen_stream_t stream);
+int gefen_lloyd_mse(const void* grad, int grad_dtype, int64_t numel, int64_t period,
+                    const float* old_codebook, const float* new_codebook, int codebook_size,
+                    float* mse_normalized_sum, float* mse_original_sum, gefen_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEFEN_HIP_H */

@@ -1,0 +1,157 @@
+"""The drop-in optimizers on the GPU against the reference's own CPU trajectories
+(golden fixtures written from ndvbd/Gefen 1.2.3 by tests/golden/make_golden.py)."""
+
+import numpy as np
+import pytest
+import torch
+
+import gpu_util as gu
+import traj_util as tu
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(params, dtype):
+    out = []
+    for prm in params:
+        t = gu.to_dev(prm["p0"].reshape(-1), dtype).reshape(prm["shape"]).clone().requires_grad_(True)
+        out.append(t)
+    return out
+
+
+def _build_gefen(meta, tensors, params):
+    from gefen_amd.gefen import Gefen
+
+    kind = meta["kind"]
+    kw = dict(meta["kwargs"])
+    named = [(prm["name"], t) for prm, t in zip(params, tensors)]
+    if kind == "gefen_groups":
+        frozen = torch.zeros(3, device="cuda:0", requires_grad=False)
+        groups = [
+            {"params": named[0:2], "lr": 3e-3, "betas": (0.8, 0.99), "weight_decay": 0.1},
+            {"params": [t for _, t in named[2:6]] + [frozen], "eps": 1e-6},
+            {"params": named[6:], "lr": 5e-4, "weight_decay": 0.01},
+        ]
+        return Gefen(groups, lr=1e-3)
+    return Gefen(named, **kw)
+
+
+@pytest.mark.parametrize("name", [n for n in tu.TRAJ_NAMES if not n.startswith("muon")])
+def test_gefen_matches_reference_trajectory(name):
+    print("trajectory", name, flush=True)
+    data, meta, params, skip = tu.build(name)
+    dtype = meta["dtype"]
+    tensors = _params(params, dtype)
+    opt = _build_gefen(meta, tensors, params)
+    if meta["kind"] != "gefen_learn":
+        opt._gefen_codebook = torch.from_numpy(data["codebook_in"]).to("cuda:0")
+    for step in range(1, meta["steps"] + 1):
+        grads = tu.grads_for(meta, params, step, skip)
+        for t, g, prm in zip(tensors, grads, params):
+            t.grad = None if g is None else gu.to_dev(g.reshape(-1), dtype).reshape(prm["shape"])
+        opt.step()
+        if step == 1:
+            assert [opt.state[t]["automatic_period"] for t in tensors] == data["periods"].tolist()
+            np.testing.assert_array_equal(opt._gefen_codebook.cpu().numpy(), data["codebook_out"])
+        if step in (1, 2, 20):
+            for i, t in enumerate(tensors):
+                st = opt.state[t]
+                key = "s{}/m_codebook/step{}".format(i, step)
+                np.testing.assert_array_equal(gu.to_np(st["m_codebook"]).reshape(-1),
+                                              tu.bits(data[key]).reshape(-1), err_msg=key)
+                key = "s{}/m_magnitude/step{}".format(i, step)
+                np.testing.assert_array_equal(gu.to_np(st["m_magnitude"]).reshape(-1),
+                                              tu.bits(data[key]).reshape(-1), err_msg=key)
+                key = "s{}/vmean/step{}".format(i, step)
+                vg = orc.to_f32(gu.to_np(st["vmean"]).reshape(-1), dtype)
+                vr = orc.to_f32(tu.bits(data[key]).reshape(-1), dtype)
+                if dtype == "f32":
+                    np.testing.assert_allclose(vg, vr, rtol=4e-6, atol=0, err_msg=key)
+                else:
+                    assert tu.ulp_distance_bf16(gu.to_np(st["vmean"]).reshape(-1),
+                                                tu.bits(data[key]).reshape(-1)).max() <= 1, key
+        if step in (1, 2, 5, 10, 20):
+            for i, t in enumerate(tensors):
+                got = gu.to_np(t).reshape(-1)
+                ref = tu.bits(data["p{}/step{}".format(i, step)]).reshape(-1)
+                if dtype == "f32":
+                    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-7,
+                                               err_msg="{} p{} step {}".format(name, i, step))
+                else:
+                    d = tu.ulp_distance_bf16(got, ref)
+                    assert d.max() <= 1, "{} p{} step {}: {} ulps".format(name, i, step, d.max())
+
+
+def test_state_dict_layout_matches_reference():
+    data, meta, params, skip = tu.build("gpt2mini_f32")
+    tensors = _params(params, "f32")
+    opt = _build_gefen(meta, tensors, params)
+    opt._gefen_codebook = torch.from_numpy(data["codebook_in"]).to("cuda:0")
+    for step in (1, 2):
+        for t, g, prm in zip(tensors, tu.grads_for(meta, params, step, skip), params):
+            t.grad = gu.to_dev(g.reshape(-1), "f32").reshape(prm["shape"])
+        opt.step()
+    sd = opt.state_dict()
+    ref = meta["state_dict"]
+    assert sorted(sd.keys()) == ref["top_keys"]
+    assert sd["gefen_global_step"] == ref["gefen_global_step"]
+    for k, v in sd["state"].items():
+        rs = ref["state"][str(k)]
+        assert sorted(v.keys()) == sorted(rs.keys()), k
+        for kk, vv in v.items():
+            if torch.is_tensor(vv):
+                assert rs[kk]["tensor"] and str(vv.dtype) == rs[kk]["dtype"] and list(vv.shape) == rs[kk]["shape"]
+            else:
+                assert not rs[kk]["tensor"] and type(vv).__name__ == rs[kk]["type"], (k, kk)
+    for g, rg in zip(sd["param_groups"], ref["param_groups"]):
+        assert sorted(g.keys()) == sorted(rg.keys())
+    # round trip into a fresh optimizer keeps dtypes and continues identically
+    tensors2 = [t.detach().clone().requires_grad_(True) for t in tensors]
+    opt2 = _build_gefen(meta, tensors2, params)
+    opt2.load_state_dict(sd)
+    for t1, t2, g, prm in zip(tensors, tensors2, tu.grads_for(meta, params, 3, skip), params):
+        gd = gu.to_dev(g.reshape(-1), "f32").reshape(prm["shape"])
+        t1.grad, t2.grad = gd, gd.clone()
+    opt.step()
+    opt2.step()
+    for t1, t2 in zip(tensors, tensors2):
+        torch.testing.assert_close(t1, t2, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("name", ["muon_bf16", "muon_f32"])
+def test_gefen_muon_matches_reference_trajectory(name):
+    from gefen_amd.gefen_muon import GefenMuon
+
+    print("trajectory", name, flush=True)
+    data, meta, params, skip = tu.build(name)
+    dtype = meta["dtype"]
+    tensors = _params(params, dtype)
+    opt = GefenMuon([(prm["name"], t) for prm, t in zip(params, tensors)], **meta["kwargs"])
+    opt._gefen_codebook = torch.from_numpy(data["codebook_in"]).to("cuda:0")
+    for step in range(1, meta["steps"] + 1):
+        grads = tu.grads_for(meta, params, step, skip)
+        for t, g, prm in zip(tensors, grads, params):
+            t.grad = gu.to_dev(g.reshape(-1), dtype).reshape(prm["shape"])
+        opt.step()
+        if step == 1:
+            assert [opt.state[t]["automatic_period"] for t in tensors] == data["periods"].tolist()
+        if step in (1, 2, 20):
+            for i, t in enumerate(tensors):
+                key = "s{}/m_codebook/step{}".format(i, step)
+                if key not in data:
+                    continue
+                np.testing.assert_array_equal(gu.to_np(opt.state[t]["m_codebook"]).reshape(-1),
+                                              tu.bits(data[key]).reshape(-1), err_msg=key)
+                key = "s{}/m_magnitude/step{}".format(i, step)
+                np.testing.assert_array_equal(gu.to_np(opt.state[t]["m_magnitude"]).reshape(-1),
+                                              tu.bits(data[key]).reshape(-1), err_msg=key)
+        if step in (1, 2, 5, 10, 20):
+            for i, (t, prm) in enumerate(zip(tensors, params)):
+                p0 = orc.to_f32(prm["p0"].reshape(-1), dtype)
+                ours = orc.to_f32(gu.to_np(t).reshape(-1), dtype) - p0
+                ref = orc.to_f32(tu.bits(data["p{}/step{}".format(i, step)]).reshape(-1), dtype) - p0
+                # Newton-Schulz: bf16 GEMMs in an accumulation order of their own (see the oracle test)
+                tol = 0.05 if dtype != "f32" else 0.01
+                rel = np.linalg.norm(ours - ref) / max(np.linalg.norm(ref), 1e-30)
+                assert rel <= tol, "{} p{} step {}: relative update error {:.3g}".format(name, i, step, rel)

@@ -1,0 +1,214 @@
+"""Parity of the fused HIP step kernels with the CPU oracle (the reference's CPU path).
+
+Codebook indices and magnitudes must be bit-exact.  vmean of period-one tensors
+is an element-wise formula and must be bit-exact too; the block mean of
+period > 1 tensors is summed in another order than torch's, so vmean agrees to
+a few fp32 ulps and the parameters to rtol 1e-5 / atol 1e-7 (fp32) or 1 ulp
+(bf16 / f16).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import gpu_util as gu
+from golden_util import load
+from gefen_amd import _lib
+from gefen_amd import synthetic as syn
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _codebook():
+    data, _ = load("exact_dp")
+    return np.ascontiguousarray(data["hist_k256_forced/codebook"], dtype=np.float32)
+
+
+def _tables(cb_dev):
+    lib = _lib.load()
+    t = torch.empty(int(lib.gefen_codebook_tables_size()), dtype=torch.uint8, device="cuda:0")
+    _lib.check(lib.gefen_prepare_codebook(cb_dev.data_ptr(), cb_dev.numel(), t.data_ptr(), gu.stream()))
+    return t
+
+
+def _ulps(a, b):
+    a = a.astype(np.int32)
+    b = b.astype(np.int32)
+    ka = np.where(a & 0x8000, 0x8000 - (a & 0x7FFF), 0x8000 + (a & 0x7FFF))
+    kb = np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + (b & 0x7FFF))
+    return np.abs(ka - kb)
+
+
+# (name, dtype, state dtype, numel, period, weight decay); periods chosen to hit every
+# kernel shape: vector widths 8/4/1, 1-8 vectors per lane, lane groups of 4..64, the
+# two-sweep path for long rows, period one, and an fp32 state for bf16 parameters.
+CASES = [
+    ("bf16_P2048", "bf16", "bf16", 2048 * 24, 2048, 0.0),
+    ("bf16_P768_wd", "bf16", "bf16", 768 * 40, 768, 0.1),
+    ("bf16_P64", "bf16", "bf16", 64 * 300, 64, 0.0),
+    ("bf16_P12", "bf16", "bf16", 12 * 500, 12, 0.0),
+    ("bf16_P9", "bf16", "bf16", 9 * 700, 9, 0.0),
+    ("bf16_P5000_long", "bf16", "bf16", 5000 * 6, 5000, 0.0),
+    ("bf16_P1", "bf16", "bf16", 256 * 50, 1, 0.0),
+    ("bf16_P1_pod250", "bf16", "bf16", 1000 * 7, 1, 0.05),
+    ("bf16_P4104_long", "bf16", "bf16", 4104 * 5, 4104, 0.0),
+    ("f32_P768", "f32", "f32", 768 * 30, 768, 0.0),
+    ("f32_P3072_long", "f32", "f32", 3072 * 5, 3072, 0.1),
+    ("f32_P1", "f32", "f32", 4096, 1, 0.0),
+    ("f32_P48", "f32", "f32", 48 * 333, 48, 0.0),
+    ("f16_P96", "f16", "f16", 96 * 128, 96, 0.0),
+    ("f16_P1", "f16", "f16", 3000, 1, 0.0),
+    ("bf16_fp32state_P256", "bf16", "f32", 256 * 64, 256, 0.0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_step_tasks_match_oracle(case):
+    name, dt, sdt, n, period, wd = case
+    print("case", name, flush=True)
+    cb = _codebook()
+    seed = sum(map(ord, name))
+    pod = orc.largest_divisor_at_most(n, 256) if period == 1 else 0
+    rows_v = n // period
+    rows_m = n // (pod if period == 1 else period)
+    p_np = syn.round_to(syn.normal(syn.make_key(seed, 1), n) * 0.02, dt)
+    p_np = p_np.view(np.uint16) if p_np.dtype == np.float16 else p_np
+    st_np = {"idx": np.zeros(n, np.uint8), "mag": np.zeros(rows_m, orc.NP_STORAGE[sdt]),
+             "v": np.zeros(rows_v, orc.NP_STORAGE[sdt])}
+    p_dev = gu.to_dev(p_np, dt)
+    idx_dev = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+    mag_dev = torch.zeros(rows_m, dtype=gu.TORCH[sdt], device="cuda:0")
+    v_dev = torch.zeros(rows_v, dtype=gu.TORCH[sdt], device="cuda:0")
+    cb_dev = torch.from_numpy(cb).to("cuda:0")
+    tables = _tables(cb_dev)
+    lib = _lib.load()
+    b1, b2, lr, eps = 0.9, 0.999, 1e-3, 1e-8
+    for step in range(1, 5):
+        grows = n // period if period > 1 else (n // 64 if n % 64 == 0 else 1)
+        g = syn.round_to(syn.row_scaled_normal(seed, step, grows, n // grows, -14, -4), dt).reshape(-1)
+        g = g.view(np.uint16) if g.dtype == np.float16 else g
+        g_dev = gu.to_dev(g, dt)
+        bc1, bc2 = 1 - b1 ** step, 1 - b2 ** step
+        task = np.zeros(1, dtype=_lib.STEP_TASK)
+        task["p"], task["grad"], task["m_codebook"] = p_dev.data_ptr(), g_dev.data_ptr(), idx_dev.data_ptr()
+        task["m_magnitude"], task["vmean"] = mag_dev.data_ptr(), v_dev.data_ptr()
+        task["numel"], task["period"], task["period_one_divisor"] = n, period, pod
+        task["param_dtype"], task["state_dtype"] = gu.CODE[dt], gu.CODE[sdt]
+        task["beta1"], task["beta2"], task["lr"], task["eps"], task["weight_decay"] = b1, b2, lr, eps, wd
+        task["bias_correction_1"], task["bias_correction_2"] = bc1, bc2
+        _lib.check(lib.gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+        rc = orc.lib().orc_gefen_step(gu.CODE[dt], gu.CODE[sdt], orc._ptr(p_np), orc._ptr(np.ascontiguousarray(g)),
+                                      orc._ptr(st_np["idx"]), orc._ptr(st_np["mag"]), orc._ptr(st_np["v"]), n, period,
+                                      pod, orc._ptr(cb), cb.size, b1, b2, lr, eps, wd, bc1, bc2, 1)
+        assert rc == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(gu.to_np(idx_dev), st_np["idx"], err_msg="{} idx step {}".format(name, step))
+        np.testing.assert_array_equal(gu.to_np(mag_dev), st_np["mag"], err_msg="{} mag step {}".format(name, step))
+        vg = orc.to_f32(gu.to_np(v_dev), sdt)
+        vo = orc.to_f32(st_np["v"], sdt)
+        if period == 1:
+            np.testing.assert_array_equal(vg, vo, err_msg="{} vmean step {}".format(name, step))
+        elif sdt == "f32":
+            np.testing.assert_allclose(vg, vo, rtol=4e-7 * 8, atol=0, err_msg="{} vmean".format(name))
+        else:
+            assert _ulps(gu.to_np(v_dev), st_np["v"]).max() <= 1
+        pg = gu.to_np(p_dev)
+        if dt == "f32":
+            np.testing.assert_allclose(pg, p_np, rtol=1e-5, atol=1e-7, err_msg="{} p step {}".format(name, step))
+            if period == 1:
+                np.testing.assert_array_equal(pg, p_np)
+        else:
+            assert _ulps(pg, p_np).max() <= 1, "{} p step {}".format(name, step)
+            if period == 1:
+                np.testing.assert_array_equal(pg, p_np)
+
+
+def test_misaligned_views_take_the_scalar_path():
+    """Parameters that start at an odd element offset still give identical indices."""
+    cb = _codebook()
+    n, period = 768 * 8, 768
+    base = syn.round_to(syn.normal(syn.make_key(3, 1), n + 1) * 0.02, "bf16")
+    p_np = base[1:].copy()
+    big = gu.to_dev(base, "bf16")
+    p_dev = big[1:]
+    g = syn.round_to(syn.row_scaled_normal(3, 2, 8, 768, -14, -4), "bf16").reshape(-1)
+    gbig = gu.to_dev(np.concatenate([np.zeros(1, np.uint16), g]), "bf16")
+    g_dev = gbig[1:]
+    idx_dev = torch.zeros(n + 1, dtype=torch.uint8, device="cuda:0")[1:]
+    mag_dev = torch.zeros(8, dtype=torch.bfloat16, device="cuda:0")
+    v_dev = torch.zeros(8, dtype=torch.bfloat16, device="cuda:0")
+    st = {"idx": np.zeros(n, np.uint8), "mag": np.zeros(8, np.uint16), "v": np.zeros(8, np.uint16)}
+    cb_dev = torch.from_numpy(cb).to("cuda:0")
+    tables = _tables(cb_dev)
+    task = np.zeros(1, dtype=_lib.STEP_TASK)
+    task["p"], task["grad"], task["m_codebook"] = p_dev.data_ptr(), g_dev.data_ptr(), idx_dev.data_ptr()
+    task["m_magnitude"], task["vmean"] = mag_dev.data_ptr(), v_dev.data_ptr()
+    task["numel"], task["period"] = n, period
+    task["param_dtype"], task["state_dtype"] = 2, 2
+    task["beta1"], task["beta2"], task["lr"], task["eps"] = 0.9, 0.999, 1e-3, 1e-8
+    task["bias_correction_1"], task["bias_correction_2"] = 0.1, 1 - 0.999
+    _lib.check(_lib.load().gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+    orc.lib().orc_gefen_step(2, 2, orc._ptr(p_np), orc._ptr(g), orc._ptr(st["idx"]), orc._ptr(st["mag"]),
+                             orc._ptr(st["v"]), n, period, 0, orc._ptr(cb), 256, 0.9, 0.999, 1e-3, 1e-8, 0.0, 0.1,
+                             1 - 0.999, 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(gu.to_np(idx_dev), st["idx"])
+    np.testing.assert_array_equal(gu.to_np(mag_dev), st["mag"])
+    assert _ulps(gu.to_np(p_dev), p_np).max() <= 1
+
+
+def test_many_tasks_in_one_call():
+    """Tensors of mixed dtypes and periods in one gefen_step_tasks call (several launches)."""
+    cb = _codebook()
+    cb_dev = torch.from_numpy(cb).to("cuda:0")
+    tables = _tables(cb_dev)
+    specs = [("bf16", 2048 * 3, 2048), ("bf16", 1024, 1), ("f32", 96 * 10, 96), ("bf16", 768 * 4, 768)] * 12
+    tasks = np.zeros(len(specs), dtype=_lib.STEP_TASK)
+    devs, oracle = [], []
+    for i, (dt, n, period) in enumerate(specs):
+        pod = orc.largest_divisor_at_most(n, 256) if period == 1 else 0
+        rows_m = n // (pod if period == 1 else period)
+        p = syn.round_to(syn.normal(syn.make_key(11, i), n) * 0.02, dt)
+        g = syn.round_to(syn.row_scaled_normal(11, 1000 + i, max(1, n // 64), 64, -14, -4), dt).reshape(-1)
+        d = {"p": gu.to_dev(p, dt), "g": gu.to_dev(g, dt), "idx": torch.zeros(n, dtype=torch.uint8, device="cuda:0"),
+             "mag": torch.zeros(rows_m, dtype=gu.TORCH[dt], device="cuda:0"),
+             "v": torch.zeros(n // period, dtype=gu.TORCH[dt], device="cuda:0")}
+        devs.append(d)
+        o = {"p": p.copy(), "g": g, "idx": np.zeros(n, np.uint8), "mag": np.zeros(rows_m, orc.NP_STORAGE[dt]),
+             "v": np.zeros(n // period, orc.NP_STORAGE[dt]), "dt": dt, "n": n, "period": period, "pod": pod}
+        oracle.append(o)
+        t = tasks[i]
+        t["p"], t["grad"], t["m_codebook"] = d["p"].data_ptr(), d["g"].data_ptr(), d["idx"].data_ptr()
+        t["m_magnitude"], t["vmean"] = d["mag"].data_ptr(), d["v"].data_ptr()
+        t["numel"], t["period"], t["period_one_divisor"] = n, period, pod
+        t["param_dtype"] = t["state_dtype"] = gu.CODE[dt]
+        t["beta1"], t["beta2"], t["lr"], t["eps"] = 0.9, 0.999, 1e-3, 1e-8
+        t["bias_correction_1"], t["bias_correction_2"] = 0.1, 1 - 0.999
+    _lib.check(_lib.load().gefen_step_tasks(tasks.ctypes.data, len(specs), tables.data_ptr(), gu.stream()))
+    for o in oracle:
+        orc.lib().orc_gefen_step(gu.CODE[o["dt"]], gu.CODE[o["dt"]], orc._ptr(o["p"]), orc._ptr(o["g"]),
+                                 orc._ptr(o["idx"]), orc._ptr(o["mag"]), orc._ptr(o["v"]), o["n"], o["period"],
+                                 o["pod"], orc._ptr(cb), 256, 0.9, 0.999, 1e-3, 1e-8, 0.0, 0.1, 1 - 0.999, 1)
+    torch.cuda.synchronize()
+    for d, o in zip(devs, oracle):
+        np.testing.assert_array_equal(gu.to_np(d["idx"]), o["idx"])
+        np.testing.assert_array_equal(gu.to_np(d["mag"]), o["mag"])
+
+
+def test_invalid_arguments_raise_value_error():
+    lib = _lib.load()
+    task = np.zeros(1, dtype=_lib.STEP_TASK)
+    x = torch.zeros(10, device="cuda:0")
+    task["p"] = task["grad"] = task["m_codebook"] = task["m_magnitude"] = task["vmean"] = x.data_ptr()
+    task["numel"], task["period"] = 10, 3
+    task["bias_correction_1"] = task["bias_correction_2"] = 0.5
+    tables = torch.zeros(int(lib.gefen_codebook_tables_size()), dtype=torch.uint8, device="cuda:0")
+    with pytest.raises(ValueError, match="does not divide"):
+        _lib.check(lib.gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+    task["period"] = 5
+    task["bias_correction_1"] = 0.0
+    with pytest.raises(ValueError, match="bias_correction_1"):
+        _lib.check(lib.gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
