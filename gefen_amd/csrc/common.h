@@ -121,4 +121,40 @@ __device__ __forceinline__ int nearest_index(float x, const float* thr, const ui
     return k;
 }
 
+
+// Exact float32 quotient a / b for a b shared by many a (a block magnitude):
+// a * RN64(1/b) in float64, rounded once to float32.  The float64 product is
+// within 2^-52 (relative) of a/b, while a quotient of two float32 numbers is
+// never a float32 rounding midpoint and lies at least 2^-49 (relative) away
+// from every midpoint (|a - m b| >= 2^e(m)+e(b) when nonzero, m b < 2^49 of
+// that unit).  Hence rounding the float64 product gives RN32(a/b), the IEEE
+// division.  rb = 1 / (double)b is computed once per block.
+__device__ __forceinline__ float div_by_block(float a, double rb) { return (float)((double)a * rb); }
+
+// |x| as an ordered integer: NaN (any payload, sign cleared) compares above inf,
+// so an unsigned max over these keys is torch's NaN-propagating absmax.
+__device__ __forceinline__ uint32_t abs_key(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Nearest codebook index of x with at most two threshold probes in the common
+// case.  The bucket is taken one below floor((x + 1) * 2048) so that the fma's
+// rounding can only move it down; its count of thresholds < edge is <= the
+// answer, and the remaining thresholds in [edge, x) are counted by probing.
+__device__ __forceinline__ int nearest_fast(float x, const float* thr, const uint16_t* bucket, int K) {
+    float y = __builtin_fmaf(x, 2048.0f, 2048.0f);
+    y = fminf(fmaxf(y, 1.0f), 4097.0f);
+    const int b = (int)y - 1;
+    int k = (x < -1.0f) ? 0 : (int)bucket[b];
+    k += (thr[k + 1] < x) ? 1 : 0;  // thr[K] = +inf stops every probe at K - 1
+    k += (thr[k + 1] < x) ? 1 : 0;
+    while (thr[k + 1] < x) ++k;    // only when three or more thresholds share the window
+    return (x != x) ? K - 1 : k;
+}
+
 }  // namespace gefen

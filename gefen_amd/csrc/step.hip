@@ -23,7 +23,7 @@
 namespace gefen {
 
 constexpr int kThreads = 256;  // 4 waves
-constexpr int kIter = 4;       // wave-units per wave in one workgroup
+constexpr int kIter = 8;       // wave-units per wave in one workgroup
 constexpr int kMaxBatch = 20;  // tasks per launch (kernel argument block < 4 KB)
 
 enum StepMode : int32_t { kVmeanUpdate = 0, kVmeanGiven = 1, kStepsizeGiven = 2 };
@@ -35,6 +35,7 @@ struct StepTask {
     void* mag;
     void* vmean;
     const float* stepsize;
+    const float* lut;  // period one, 16-bit state: stepsize of every non-negative state value
     int64_t nrows;     // magnitude rows
     int64_t rowlen;    // elements per magnitude row
     int32_t period;    // elements per vmean row (rowlen if P > 1, 1 if P = 1)
@@ -88,6 +89,15 @@ __device__ __forceinline__ float stepsize_of(float v, const StepTask& T) {
 // ---------------------------------------------------------------------------
 // Gefen step, register path.  QROUND: the dequantised update cb[idx]*mag is
 // rounded to D (param dtype == state dtype) or kept in fp32 (fp32 state).
+template <typename S>
+__device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
+    if constexpr (sizeof(S) == 2) {
+        const uint16_t bits = reinterpret_cast<const uint16_t&>(v);
+        if (T.lut && !(bits & 0x8000u)) return T.lut[bits];
+    }
+    return stepsize_of(to_f32(v), T);
+}
+
 template <typename D, typename S, int W, int R, bool P1>
 __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     __shared__ LdsTables L;
@@ -122,7 +132,8 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
         Vec<uint8_t, W> iv[R];
         Vec<S, W> vv[R];
         float upd[R][W];
-        float mx = 0.0f, sumsq = 0.0f;
+        uint32_t mxk = 0;
+        float sumsq = 0.0f;
         const float mold = active ? to_f32(mag[row]) : 0.0f;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
@@ -143,9 +154,10 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
                 for (int w = 0; w < W; ++w) {
                     const float gf = to_f32(gv[j].v[w]);
                     const float cur = L.cbd[iv[j].v[w]] * mold;
-                    const float u = __builtin_fmaf(T.b1c, gf - cur, cur);  // lerp, w < 0.5
+                    const float u = __builtin_fmaf(T.b1c, gf - cur, cur);  // lerp, weight < 0.5
                     upd[j][w] = u;
-                    mx = nanmax(mx, fabsf(u));
+                    const uint32_t key = abs_key(u);
+                    mxk = key > mxk ? key : mxk;
                     if (!P1) {
                         const float sq = gf * gf;
                         sumsq = sumsq + sq;
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
                 }
             }
         }
-        mx = group_max(mx, lpr);
+        const float mx = __uint_as_float(group_max_u32(mxk, lpr));
         float ss = 0.0f;
         if (!P1) {
             if (T.mode == kVmeanUpdate) {
@@ -175,6 +187,9 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
         const S mag_s = from_f32<S>(mx);
         if (lir == 0) mag[row] = mag_s;
         const float mn = to_f32(mag_s);
+        // x = upd / mn where mn > 0, else 0 (gefen.py:1184-1187)
+        const double rb = (mn > 0.0f) ? 1.0 / (double)mn : 0.0;
+        const bool nan_block = mn != mn;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             const int v = lir + j * lpr;
@@ -185,8 +200,9 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
                 Vec<S, W> vo;
 #pragma unroll
                 for (int w = 0; w < W; ++w) {
-                    const float x = (mn > 0.0f) ? upd[j][w] / mn : 0.0f;
-                    const int k = nearest_index(x, L.thr, L.bucket, K);
+                    float x = div_by_block(upd[j][w], rb);
+                    if (nan_block) x = 0.0f;
+                    const int k = nearest_fast(x, L.thr, L.bucket, K);
                     io.v[w] = (uint8_t)k;
                     float q = L.cbd[k] * mn;
                     if (QROUND) q = round_to<D>(q);
@@ -197,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
                         const float prev = to_f32(vv[j].v[w]) * T.b2;
                         const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
                         vo.v[w] = vnew;
-                        s = stepsize_of(to_f32(vnew), T);
+                        s = p1_stepsize<S>(vnew, T);
                     }
                     const float u = (q * s) * T.lr;
                     float pf = to_f32(pv[j].v[w]);
@@ -271,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step_long(const StepBatch B)
         const float cur = L.cbd[idx[base + j]] * mold;
         const float u = __builtin_fmaf(T.b1c, gf - cur, cur);
         const float x = (mn > 0.0f) ? u / mn : 0.0f;
-        const int k = nearest_index(x, L.thr, L.bucket, K);
+        const int k = nearest_fast(x, L.thr, L.bucket, K);
         idx[base + j] = (uint8_t)k;
         float q = L.cbd[k] * mn;
         if (QROUND) q = round_to<D>(q);
@@ -388,7 +404,7 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
                 for (int w = 0; w < W; ++w) {
                     float x = round_to<D>(mu[j][w] / clamped);  // div_
                     if (ms <= 0.0f) x = 0.0f;                   // masked_fill_(mag <= 0)
-                    const int k = nearest_index(x, L.thr, L.bucket, K);
+                    const int k = nearest_fast(x, L.thr, L.bucket, K);
                     io.v[w] = (uint8_t)k;
                     const float q = round_to<D>(L.cbd[k] * ms);  // copy_(cb[idx]) then mul_(mag)
                     oo.v[w] = from_f32<D>(muon_out<D, S>(q, to_f32(gv[j].v[w]), T));
@@ -438,10 +454,25 @@ __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
         const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));
         float x = round_to<D>(m1 / clamped);
         if (ms <= 0.0f) x = 0.0f;
-        const int k = nearest_index(x, L.thr, L.bucket, K);
+        const int k = nearest_fast(x, L.thr, L.bucket, K);
         idx[base + j] = (uint8_t)k;
         const float q = round_to<D>(L.cbd[k] * ms);
         out[base + j] = from_f32<D>(muon_out<D, S>(q, gf, T));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Stepsize table of a period-one tensor with a 16-bit state: lut[b] is the
+// stepsize (gefen.py:1326-1327) of the non-negative state value with bits b,
+// computed by the same expression as the per-block path, so lookups are exact.
+template <typename S>
+__global__ __launch_bounds__(256) void k_build_lut(float* __restrict__ lut, StepTask T) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < 32768) {
+        S v;
+        const uint16_t bits = (uint16_t)i;
+        __builtin_memcpy(&v, &bits, 2);
+        lut[i] = stepsize_of(to_f32(v), T);
     }
 }
 
@@ -671,6 +702,51 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     return GEFEN_OK;
 }
 
+// Build the stepsize tables of the period-one tasks with a 16-bit state (one
+// table per distinct (dtype, sqrt(bc2), eps, 1/bc1)); *buf owns them until the
+// launches that read them are enqueued.
+int prepare_luts(std::vector<PendingStep>& pend, hipStream_t st, void** buf) {
+    struct LutKey { int s; float a, b, c; };
+    std::vector<LutKey> keys;
+    std::vector<int> which(pend.size(), -1);
+    for (size_t i = 0; i < pend.size(); ++i) {
+        const Key& k = pend[i].key;
+        if (!k.p1 || k.s == GEFEN_F32) continue;
+        const StepTask& t = pend[i].task;
+        int found = -1;
+        for (size_t j = 0; j < keys.size(); ++j)
+            if (keys[j].s == k.s && memcmp(&keys[j].a, &t.sqrt_bc2, 4) == 0 && memcmp(&keys[j].b, &t.eps, 4) == 0 &&
+                memcmp(&keys[j].c, &t.inv_bc1, 4) == 0)
+                found = (int)j;
+        if (found < 0) {
+            found = (int)keys.size();
+            keys.push_back(LutKey{k.s, t.sqrt_bc2, t.eps, t.inv_bc1});
+        }
+        which[i] = found;
+    }
+    *buf = nullptr;
+    if (keys.empty()) return GEFEN_OK;
+    hipError_t e = hipMallocAsync(buf, keys.size() * 32768 * sizeof(float), st);
+    if (e != hipSuccess) return hip_status(e, "hipMallocAsync(stepsize tables)");
+    float* base = static_cast<float*>(*buf);
+    for (size_t j = 0; j < keys.size(); ++j) {
+        StepTask t;
+        memset(&t, 0, sizeof(t));
+        t.sqrt_bc2 = keys[j].a;
+        t.eps = keys[j].b;
+        t.inv_bc1 = keys[j].c;
+        if (keys[j].s == GEFEN_BF16)
+            hipLaunchKernelGGL(k_build_lut<bf16_t>, dim3(128), dim3(256), 0, st, base + j * 32768, t);
+        else
+            hipLaunchKernelGGL(k_build_lut<f16_t>, dim3(128), dim3(256), 0, st, base + j * 32768, t);
+        int rc = launch_status("gefen stepsize table");
+        if (rc) return rc;
+    }
+    for (size_t i = 0; i < pend.size(); ++i)
+        if (which[i] >= 0) pend[i].task.lut = base + (size_t)which[i] * 32768;
+    return GEFEN_OK;
+}
+
 int check_step_task(const gefen_step_task& t) {
     if (t.numel < 0) return fail_inval("numel must be non-negative");
     if (!valid_pair(t.param_dtype, t.state_dtype))
@@ -725,7 +801,12 @@ extern "C" int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const 
         if (rc) return rc;
         pend.push_back(ps);
     }
-    return flush_steps(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    void* luts = nullptr;
+    int rc = prepare_luts(pend, st, &luts);
+    if (rc == GEFEN_OK) rc = flush_steps(pend, static_cast<const CodebookTables*>(tables), st);
+    if (luts) (void)hipFreeAsync(luts, st);
+    return rc;
 }
 
 static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign, void* mag,
@@ -772,7 +853,11 @@ static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_
     rc = tt.init(codebook, K, st);
     if (rc) return rc;
     std::vector<PendingStep> pend(1, ps);
-    return flush_steps(pend, static_cast<const CodebookTables*>(tt.ptr), st);
+    void* luts = nullptr;
+    rc = prepare_luts(pend, st, &luts);
+    if (rc == GEFEN_OK) rc = flush_steps(pend, static_cast<const CodebookTables*>(tt.ptr), st);
+    if (luts) (void)hipFreeAsync(luts, st);
+    return rc;
 }
 
 extern "C" int gefen_automatic_fused_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,
