@@ -29,6 +29,8 @@ __device__ __forceinline__ float f_dec(int32_t o) {
 __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restrict__ cb, int K,
                                                           CodebookTables* __restrict__ T) {
     __shared__ float thr[260];
+    __shared__ uint16_t bk[4100];
+    __shared__ int probe_max;
     const int t = threadIdx.x;
     T->cb[t] = t < K ? cb[t] : __builtin_inff();
     if (t == 0) T->K = K;
@@ -68,7 +70,21 @@ __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restric
             c = (uint16_t)(lo - 1);
         }
         T->bucket[e] = c;
+        bk[e] = c;
     }
+    if (t == 0) probe_max = 0;
+    __syncthreads();
+    // a search from bucket b (one below x's bucket) meets the thresholds in
+    // [edge_b, edge_b+2); past the last edges it meets every finite one left
+    int worst = 0;
+    for (int b = t; b <= 4096; b += 256) {
+        const int hi = (b + 2 <= 4096) ? (int)bk[b + 2] : (K - 1);
+        const int n = hi - (int)bk[b];
+        worst = n > worst ? n : worst;
+    }
+    atomicMax(&probe_max, worst);
+    __syncthreads();
+    if (t == 0) T->max_probe = (bk[0] != 0) ? 1 << 20 : probe_max;
 }
 
 // ---------------------------------------------------------------------------

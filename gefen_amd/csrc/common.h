@@ -97,12 +97,16 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 //            picks the left entry, or cb[k-1] if none; thr[K] = +inf sentinel.
 //            The nearest index of a non-NaN x is #{k in 1..K-1 : thr[k] < x}.
 //   bucket[e] for e = 0..4096: #{k : thr[k] < -1 + e/2048}.
+//   max_probe: most thresholds a search started one bucket low can meet before
+//            reaching x (0 if thresholds lie below -1); <= 2 lets the kernels
+//            use the fixed two-probe search.
 struct CodebookTables {
     float cb[256];
     float thr[260];
     uint16_t bucket[4100];
     int32_t K;
-    int32_t pad[3];
+    int32_t max_probe;
+    int32_t pad[2];
 };
 
 // Nearest codebook index (gefen.py:122-143) from LDS copies of thr and bucket.

@@ -98,11 +98,84 @@ __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
     return stepsize_of(to_f32(v), T);
 }
 
-template <typename D, typename S, int W, int R, bool P1>
+// Nearest index with at most two threshold probes (max_probe <= 2): one
+// ds_read2 of thr[k+1], thr[k+2] after the bucket lookup.
+__device__ __forceinline__ int nearest_two_probe(float x, const float* thr, const uint16_t* bucket) {
+    float y = __builtin_fmaf(x, 2048.0f, 2047.0f);  // (x + 1) * 2048 - 1, rounded once
+    y = fminf(fmaxf(y, 0.0f), 4096.0f);
+    int k = bucket[(int)y];
+    const float t1 = thr[k + 1], t2 = thr[k + 2];
+    k += (t1 < x ? 1 : 0) + (t2 < x ? 1 : 0);
+    return k;
+}
+
+// Second sweep of a row: quantise, dequantise, update p.  FAST: the block
+// magnitude is finite and positive and the two-probe search is exact.
+template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST>
+__device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
+                                            const float (&upd)[R][W], const Vec<D, W> (&gv)[R],
+                                            const Vec<D, W> (&pv)[R], const Vec<S, W> (&vv)[R], uint8_t* idx, D* p,
+                                            S* vm, int64_t base, int lir, int lpr, int K, float mn, double rb,
+                                            float ss) {
+    constexpr bool QROUND = sizeof(D) == sizeof(S);
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int v = lir + j * lpr;
+        if (v < T.nvec) {
+            const int64_t e = base + (int64_t)v * W;
+            Vec<uint8_t, W> io;
+            Vec<D, W> po;
+            Vec<S, W> vo;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                int k;
+                if (FAST) {
+                    k = nearest_two_probe(div_by_block(upd[j][w], rb), L.thr, L.bucket);
+                } else {
+                    const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
+                    const float x = plain ? div_by_block(upd[j][w], rb) : ((mn > 0.0f) ? upd[j][w] / mn : 0.0f);
+                    k = nearest_fast(x, L.thr, L.bucket, K);
+                }
+                io.v[w] = (uint8_t)k;
+                float u;
+                if (TAB && !P1 && FAST) {
+                    u = utab[k];
+                } else {
+                    float q = L.cbd[k] * mn;
+                    if (QROUND) q = round_to<D>(q);
+                    float s = ss;
+                    if (P1) {
+                        const float gf = to_f32(gv[j].v[w]);
+                        const float sq = gf * gf;  // mean over a one-element row
+                        const float prev = to_f32(vv[j].v[w]) * T.b2;
+                        const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
+                        vo.v[w] = vnew;
+                        s = p1_stepsize<S>(vnew, T);
+                    }
+                    u = (q * s) * T.lr;
+                }
+                float pf = to_f32(pv[j].v[w]);
+                if (T.do_wd) pf = round_to<D>(pf * T.wdf);
+                po.v[w] = from_f32<D>(pf - u);
+            }
+            vstore<uint8_t, W>(idx, e, io);
+            vstore<D, W>(p, e, po);
+            if (P1) vstore<S, W>(vm, e, vo);
+        }
+    }
+}
+
+// TAB: a lane group of >= 32 lanes owns the row and keeps two row tables in
+// LDS, cur[i] = cb_D[i] * old magnitude and upd[i] = the parameter step of
+// codeword i (gefen.py:1205-1206, 1328-1332 for this row's magnitude and
+// stepsize), so the element loops look both up instead of recomputing.
+template <typename D, typename S, int W, int R, bool P1, bool TAB>
 __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     __shared__ LdsTables L;
+    __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
     int K;
     load_tables<D>(L, B.tables, K);
+    const bool two_probe = B.tables->max_probe <= 2;
     const int ti = find_task(B.wg_begin, B.ntasks);
     const StepTask& T = B.t[ti];
     constexpr bool QROUND = sizeof(D) == sizeof(S);
@@ -114,6 +187,8 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     const int lir = lane & (lpr - 1);
     const int sub = lane >> T.lpr_log2;
     const int64_t lw = blockIdx.x - B.wg_begin[ti];
+    float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
+    float* utab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
 
     D* __restrict__ p = static_cast<D*>(T.p);
     const D* __restrict__ g = static_cast<const D*>(T.g);
@@ -146,6 +221,14 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
                 if (P1) vv[j] = vload<S, W>(vm, e);
             }
         }
+        if (TAB) {
+            __builtin_amdgcn_wave_barrier();
+            if (active)
+                for (int i = lir; i < 256; i += lpr) ctab[i] = L.cbd[i] * mold;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             const int v = lir + j * lpr;
@@ -153,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
 #pragma unroll
                 for (int w = 0; w < W; ++w) {
                     const float gf = to_f32(gv[j].v[w]);
-                    const float cur = L.cbd[iv[j].v[w]] * mold;
+                    const float cur = TAB ? ctab[iv[j].v[w]] : L.cbd[iv[j].v[w]] * mold;
                     const float u = __builtin_fmaf(T.b1c, gf - cur, cur);  // lerp, weight < 0.5
                     upd[j][w] = u;
                     const uint32_t key = abs_key(u);
@@ -187,43 +270,29 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
         const S mag_s = from_f32<S>(mx);
         if (lir == 0) mag[row] = mag_s;
         const float mn = to_f32(mag_s);
-        // x = upd / mn where mn > 0, else 0 (gefen.py:1184-1187)
-        const double rb = (mn > 0.0f) ? 1.0 / (double)mn : 0.0;
-        const bool nan_block = mn != mn;
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            const int v = lir + j * lpr;
-            if (v < T.nvec) {
-                const int64_t e = base + (int64_t)v * W;
-                Vec<uint8_t, W> io;
-                Vec<D, W> po;
-                Vec<S, W> vo;
-#pragma unroll
-                for (int w = 0; w < W; ++w) {
-                    float x = div_by_block(upd[j][w], rb);
-                    if (nan_block) x = 0.0f;
-                    const int k = nearest_fast(x, L.thr, L.bucket, K);
-                    io.v[w] = (uint8_t)k;
-                    float q = L.cbd[k] * mn;
+        // x = upd / mn where mn > 0, else 0 (gefen.py:1184-1187).  A block whose
+        // magnitude is 0, NaN or inf takes the general element path.
+        const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
+        const double rb = plain ? 1.0 / (double)mn : 0.0;
+        const bool fast = plain && two_probe;
+        if (TAB && !P1) {
+            if (fast) {
+                for (int i = lir; i < 256; i += lpr) {
+                    float q = L.cbd[i] * mn;
                     if (QROUND) q = round_to<D>(q);
-                    float s = ss;
-                    if (P1) {
-                        const float gf = to_f32(gv[j].v[w]);
-                        const float sq = gf * gf;  // mean over a one-element row
-                        const float prev = to_f32(vv[j].v[w]) * T.b2;
-                        const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
-                        vo.v[w] = vnew;
-                        s = p1_stepsize<S>(vnew, T);
-                    }
-                    const float u = (q * s) * T.lr;
-                    float pf = to_f32(pv[j].v[w]);
-                    if (T.do_wd) pf = round_to<D>(pf * T.wdf);
-                    po.v[w] = from_f32<D>(pf - u);
+                    utab[i] = (q * ss) * T.lr;
                 }
-                vstore<uint8_t, W>(idx, e, io);
-                vstore<D, W>(p, e, po);
-                if (P1) vstore<S, W>(vm, e, vo);
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        if (fast) {
+            step_sweep2<D, S, W, R, P1, TAB, true>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, K, mn, rb,
+                                                   ss);
+        } else {
+            step_sweep2<D, S, W, R, P1, TAB, false>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, K, mn,
+                                                    rb, ss);
         }
     }
 }
@@ -544,17 +613,23 @@ int r_bucket(int64_t nvec, int lpr_log2) {
 
 // kernel key: dtype pair, W, R (0 = long rows), P1
 struct Key {
-    int d, s, W, R, p1;
-    bool operator==(const Key& o) const { return d == o.d && s == o.s && W == o.W && R == o.R && p1 == o.p1; }
+    int d, s, W, R, p1, tab;
+    bool operator==(const Key& o) const {
+        return d == o.d && s == o.s && W == o.W && R == o.R && p1 == o.p1 && tab == o.tab;
+    }
 };
 
 template <typename D, typename S>
 hipError_t launch_step(const Key& k, const StepBatch& b, int grid, hipStream_t st) {
-#define GEFEN_STEP_CASE(WW, RR)                                                                  \
-    if (k.W == WW && k.R == RR) {                                                               \
-        if (k.p1) hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, true>), dim3(grid), dim3(kThreads), 0, st, b); \
-        else hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false>), dim3(grid), dim3(kThreads), 0, st, b);     \
-        return hipGetLastError();                                                               \
+#define GEFEN_STEP_CASE(WW, RR)                                                                          \
+    if (k.W == WW && k.R == RR) {                                                                       \
+        if (k.p1) {                                                                                     \
+            hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, true, false>), dim3(grid), dim3(kThreads), 0, st, b);           \
+        } else {                                                                                        \
+            if (k.tab) hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false, true>), dim3(grid), dim3(kThreads), 0, st, b); \
+            else hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false, false>), dim3(grid), dim3(kThreads), 0, st, b);      \
+        }                                                                                               \
+        return hipGetLastError();                                                                       \
     }
     if (k.R == 0) {
         hipLaunchKernelGGL((k_gefen_step_long<D, S>), dim3(grid), dim3(kThreads), 0, st, b);
@@ -673,7 +748,9 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     const int l2 = lpr_log2_for(nvec);
     int R = r_bucket(nvec, l2);
     if (p1 && R == 0) return fail_inval("period_one_divisor %lld is too large", (long long)rowlen);
-    Key k{in.param_dtype, in.state_dtype, R == 0 ? 1 : W, R, p1 ? 1 : 0};
+    // row tables pay off when a row has at least as many elements as codewords per lane group
+    const int tab = (R != 0 && l2 >= 5 && !p1) ? 1 : 0;
+    Key k{in.param_dtype, in.state_dtype, R == 0 ? 1 : W, R, p1 ? 1 : 0, tab};
     StepTask& t = out.task;
     memset(&t, 0, sizeof(t));
     t.p = in.p;
@@ -918,7 +995,7 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     const int64_t nvec = rowlen / W;
     const int l2 = lpr_log2_for(nvec);
     const int R = r_bucket(nvec, l2);
-    Key k{in.grad_dtype, in.state_dtype, R == 0 ? 1 : W, R, 0};
+    Key k{in.grad_dtype, in.state_dtype, R == 0 ? 1 : W, R, 0, 0};
     MuonTask& t = out.task;
     memset(&t, 0, sizeof(t));
     t.g = in.grad;

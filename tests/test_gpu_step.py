@@ -126,6 +126,62 @@ def test_step_tasks_match_oracle(case):
                 np.testing.assert_array_equal(pg, p_np)
 
 
+def _special_codebook(kind):
+    if kind == "dense":   # codewords closer than the 4096-bucket width: the probing loop path
+        cb = np.concatenate([[-1.0], np.linspace(-0.06, 0.06, 254), [1.0]]).astype(np.float32)
+    elif kind == "wide":  # entries beyond [-1, 1] (a loaded, not learned, codebook)
+        cb = np.sort(np.concatenate([np.linspace(-2.0, 2.0, 200), np.linspace(-0.1, 0.1, 56)])).astype(np.float32)
+    else:                 # padded codebook with repeated entries
+        cb = np.sort(np.concatenate([[-1.0, 1.0], np.repeat(np.linspace(-0.5, 0.5, 9), 28)[:254]])).astype(np.float32)
+    return np.ascontiguousarray(cb)
+
+
+@pytest.mark.parametrize("kind", ["dense", "wide", "repeated"])
+@pytest.mark.parametrize("dt,period", [("bf16", 2048), ("bf16", 256), ("f32", 96), ("bf16", 1)])
+def test_step_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, period):
+    """General search path (many thresholds per bucket, thresholds below -1,
+    duplicate codewords) and rows whose magnitude is 0, inf or NaN."""
+    print("case", kind, dt, period, flush=True)
+    cb = _special_codebook(kind)
+    n = (period if period > 1 else 256) * 16
+    pod = orc.largest_divisor_at_most(n, 256) if period == 1 else 0
+    rows_m = n // (pod if period == 1 else period)
+    rows_v = n // period
+    p_np = syn.round_to(syn.normal(syn.make_key(77, 1), n) * 0.02, dt)
+    st_np = {"idx": np.zeros(n, np.uint8), "mag": np.zeros(rows_m, orc.NP_STORAGE[dt]),
+             "v": np.zeros(rows_v, orc.NP_STORAGE[dt])}
+    p_dev = gu.to_dev(p_np, dt)
+    idx_dev = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+    mag_dev = torch.zeros(rows_m, dtype=gu.TORCH[dt], device="cuda:0")
+    v_dev = torch.zeros(rows_v, dtype=gu.TORCH[dt], device="cuda:0")
+    tables = _tables(torch.from_numpy(cb).to("cuda:0"))
+    lib = _lib.load()
+    blk = pod if period == 1 else period
+    for step in range(1, 4):
+        g = syn.round_to(syn.row_scaled_normal(78, step, n // blk, blk, -14, -4), dt).reshape(-1).copy()
+        if step == 1:
+            g[:blk] = 0                      # zero magnitude block
+        if step == 2:
+            g[blk + 3] = np.float32(np.inf) if dt == "f32" else 0x7F80  # inf magnitude block
+            g[2 * blk + 5] = np.float32(np.nan) if dt == "f32" else 0x7FC0  # NaN block
+        g_dev = gu.to_dev(g, dt)
+        bc1, bc2 = 1 - 0.9 ** step, 1 - 0.999 ** step
+        task = np.zeros(1, dtype=_lib.STEP_TASK)
+        task["p"], task["grad"], task["m_codebook"] = p_dev.data_ptr(), g_dev.data_ptr(), idx_dev.data_ptr()
+        task["m_magnitude"], task["vmean"] = mag_dev.data_ptr(), v_dev.data_ptr()
+        task["numel"], task["period"], task["period_one_divisor"] = n, period, pod
+        task["param_dtype"] = task["state_dtype"] = gu.CODE[dt]
+        task["beta1"], task["beta2"], task["lr"], task["eps"] = 0.9, 0.999, 1e-3, 1e-8
+        task["bias_correction_1"], task["bias_correction_2"] = bc1, bc2
+        _lib.check(lib.gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+        orc.lib().orc_gefen_step(gu.CODE[dt], gu.CODE[dt], orc._ptr(p_np), orc._ptr(g), orc._ptr(st_np["idx"]),
+                                 orc._ptr(st_np["mag"]), orc._ptr(st_np["v"]), n, period, pod, orc._ptr(cb), cb.size,
+                                 0.9, 0.999, 1e-3, 1e-8, 0.0, bc1, bc2, 1)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(gu.to_np(idx_dev), st_np["idx"], err_msg="idx step {}".format(step))
+        np.testing.assert_array_equal(gu.to_np(mag_dev), st_np["mag"], err_msg="mag step {}".format(step))
+
+
 def test_misaligned_views_take_the_scalar_path():
     """Parameters that start at an odd element offset still give identical indices."""
     cb = _codebook()
