@@ -209,6 +209,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also copy 2 GiB device-to-device once (a known-size kernel for HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
@@ -220,6 +222,12 @@ def main():
     from gefen_amd.gefen_muon import GefenMuon
     from gefen_amd import _lib
 
+    if args.copy_probe:
+        src = torch.empty(1 << 30, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     params = build_problem(cfg, dev)
     Opt = GefenMuon if cfg["opt"] == "muon" else Gefen
     opt = Opt(params)

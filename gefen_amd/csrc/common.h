@@ -77,6 +77,19 @@ template <typename T, int W>
 __device__ __forceinline__ void vstore(T* base, int64_t elem, const Vec<T, W>& x) {
     *reinterpret_cast<Vec<T, W>*>(base + elem) = x;
 }
+// Same with a wave-uniform base and a 32-bit element offset: global memory
+// instructions take the base from scalar registers and the byte offset from
+// one vector register.
+template <typename T, int W>
+__device__ __forceinline__ Vec<T, W> vload32(const T* base, uint32_t elem) {
+    const uint32_t off = elem * (uint32_t)sizeof(T);
+    return *reinterpret_cast<const Vec<T, W>*>(reinterpret_cast<const char*>(base) + off);
+}
+template <typename T, int W>
+__device__ __forceinline__ void vstore32(T* base, uint32_t elem, const Vec<T, W>& x) {
+    const uint32_t off = elem * (uint32_t)sizeof(T);
+    *reinterpret_cast<Vec<T, W>*>(reinterpret_cast<char*>(base) + off) = x;
+}
 
 // ----------------------------------------------------------------- wave reductions
 // Butterfly over groups of `width` lanes (width a power of two <= 64).

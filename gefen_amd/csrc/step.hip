@@ -110,57 +110,59 @@ __device__ __forceinline__ int nearest_two_probe(float x, const float* thr, cons
 }
 
 // Second sweep of a row: quantise, dequantise, update p.  FAST: the block
-// magnitude is finite and positive and the two-probe search is exact.
+// magnitude is finite and positive and the two-probe search is exact.  Every
+// lane computes all R vectors (out-of-row vectors hold a copy of the row's last
+// vector); only in-row vectors of active rows are stored.
 template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST>
 __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
                                             const float (&upd)[R][W], const Vec<D, W> (&gv)[R],
                                             const Vec<D, W> (&pv)[R], const Vec<S, W> (&vv)[R], uint8_t* idx, D* p,
-                                            S* vm, int64_t base, int lir, int lpr, int K, float mn, double rb,
-                                            float ss) {
+                                            S* vm, uint32_t base, int lir, int lpr, bool active, int K, float mn,
+                                            double rb, float ss) {
     constexpr bool QROUND = sizeof(D) == sizeof(S);
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-        const int v = lir + j * lpr;
-        if (v < T.nvec) {
-            const int64_t e = base + (int64_t)v * W;
-            Vec<uint8_t, W> io;
-            Vec<D, W> po;
-            Vec<S, W> vo;
+        Vec<uint8_t, W> io;
+        Vec<D, W> po;
+        Vec<S, W> vo;
 #pragma unroll
-            for (int w = 0; w < W; ++w) {
-                int k;
-                if (FAST) {
-                    k = nearest_two_probe(div_by_block(upd[j][w], rb), L.thr, L.bucket);
-                } else {
-                    const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
-                    const float x = plain ? div_by_block(upd[j][w], rb) : ((mn > 0.0f) ? upd[j][w] / mn : 0.0f);
-                    k = nearest_fast(x, L.thr, L.bucket, K);
-                }
-                io.v[w] = (uint8_t)k;
-                float u;
-                if (TAB && !P1 && FAST) {
-                    u = utab[k];
-                } else {
-                    float q = L.cbd[k] * mn;
-                    if (QROUND) q = round_to<D>(q);
-                    float s = ss;
-                    if (P1) {
-                        const float gf = to_f32(gv[j].v[w]);
-                        const float sq = gf * gf;  // mean over a one-element row
-                        const float prev = to_f32(vv[j].v[w]) * T.b2;
-                        const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
-                        vo.v[w] = vnew;
-                        s = p1_stepsize<S>(vnew, T);
-                    }
-                    u = (q * s) * T.lr;
-                }
-                float pf = to_f32(pv[j].v[w]);
-                if (T.do_wd) pf = round_to<D>(pf * T.wdf);
-                po.v[w] = from_f32<D>(pf - u);
+        for (int w = 0; w < W; ++w) {
+            int k;
+            if (FAST) {
+                k = nearest_two_probe(div_by_block(upd[j][w], rb), L.thr, L.bucket);
+            } else {
+                const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
+                const float x = plain ? div_by_block(upd[j][w], rb) : ((mn > 0.0f) ? upd[j][w] / mn : 0.0f);
+                k = nearest_fast(x, L.thr, L.bucket, K);
             }
-            vstore<uint8_t, W>(idx, e, io);
-            vstore<D, W>(p, e, po);
-            if (P1) vstore<S, W>(vm, e, vo);
+            io.v[w] = (uint8_t)k;
+            float u;
+            if (TAB && !P1 && FAST) {
+                u = utab[k];
+            } else {
+                float q = L.cbd[k] * mn;
+                if (QROUND) q = round_to<D>(q);
+                float s = ss;
+                if (P1) {
+                    const float gf = to_f32(gv[j].v[w]);
+                    const float sq = gf * gf;  // mean over a one-element row
+                    const float prev = to_f32(vv[j].v[w]) * T.b2;
+                    const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
+                    vo.v[w] = vnew;
+                    s = p1_stepsize<S>(vnew, T);
+                }
+                u = (q * s) * T.lr;
+            }
+            float pf = to_f32(pv[j].v[w]);
+            if (T.do_wd) pf = round_to<D>(pf * T.wdf);
+            po.v[w] = from_f32<D>(pf - u);
+        }
+        const int v = lir + j * lpr;
+        if (active && v < T.nvec) {
+            const uint32_t e = base + (uint32_t)(v * W);
+            vstore32<uint8_t, W>(idx, e, io);
+            vstore32<D, W>(p, e, po);
+            if (P1) vstore32<S, W>(vm, e, vo);
         }
     }
 }
@@ -169,6 +171,11 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
 // LDS, cur[i] = cb_D[i] * old magnitude and upd[i] = the parameter step of
 // codeword i (gefen.py:1205-1206, 1328-1332 for this row's magnitude and
 // stepsize), so the element loops look both up instead of recomputing.
+//
+// Loads are unconditional and straight-line: a lane group past the last row
+// reads the last row, a vector past the row end reads the row's last vector,
+// so each lane has all of its row's bytes in flight at once.  Absmax is
+// idempotent under such copies; the sum of squares masks them out.
 template <typename D, typename S, int W, int R, bool P1, bool TAB>
 __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     __shared__ LdsTables L;
@@ -177,11 +184,10 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     load_tables<D>(L, B.tables, K);
     const bool two_probe = B.tables->max_probe <= 2;
     const int ti = find_task(B.wg_begin, B.ntasks);
-    const StepTask& T = B.t[ti];
-    constexpr bool QROUND = sizeof(D) == sizeof(S);
+    const StepTask T = B.t[ti];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lpr = 1 << T.lpr_log2;
     const int rpw = 64 >> T.lpr_log2;
     const int lir = lane & (lpr - 1);
@@ -190,85 +196,93 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
     float* utab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
 
-    D* __restrict__ p = static_cast<D*>(T.p);
-    const D* __restrict__ g = static_cast<const D*>(T.g);
-    uint8_t* __restrict__ idx = T.idx;
-    S* __restrict__ mag = static_cast<S*>(T.mag);
-    S* __restrict__ vm = static_cast<S*>(T.vmean);
-
     for (int it = 0; it < kIter; ++it) {
         const int64_t unit = (lw * kIter + it) * 4 + wave;
-        const int64_t row = unit * rpw + sub;
-        if (unit * rpw >= T.nrows) break;  // uniform across the wave
+        const int64_t row0 = unit * rpw;
+        if (row0 >= T.nrows) break;  // uniform across the wave
+        const int64_t row = row0 + sub;
         const bool active = row < T.nrows;
-        const int64_t base = row * T.rowlen;
+        const int rsub = active ? sub : (int)(T.nrows - 1 - row0);  // row within the unit
+        // the unit's rows start here; lanes address them with 32-bit offsets
+        // (64 rows of at most 64 * 8 * 8 elements)
+        const int64_t ub = row0 * T.rowlen;
+        D* __restrict__ p = static_cast<D*>(T.p) + ub;
+        const D* __restrict__ g = static_cast<const D*>(T.g) + ub;
+        uint8_t* __restrict__ idx = T.idx + ub;
+        S* __restrict__ mag = static_cast<S*>(T.mag) + row0;
+        S* __restrict__ vm = static_cast<S*>(T.vmean) + (P1 ? ub : row0);
+        const float* stepsize = T.stepsize + row0;
+        const uint32_t base = (uint32_t)rsub * (uint32_t)T.rowlen;
 
+        // every element vector of the row, then the row scalars
         Vec<D, W> gv[R], pv[R];
         Vec<uint8_t, W> iv[R];
         Vec<S, W> vv[R];
-        float upd[R][W];
-        uint32_t mxk = 0;
-        float sumsq = 0.0f;
-        const float mold = active ? to_f32(mag[row]) : 0.0f;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-            const int v = lir + j * lpr;
-            if (active && v < T.nvec) {
-                const int64_t e = base + (int64_t)v * W;
-                gv[j] = vload<D, W>(g, e);
-                iv[j] = vload<uint8_t, W>(idx, e);
-                pv[j] = vload<D, W>(p, e);
-                if (P1) vv[j] = vload<S, W>(vm, e);
-            }
+            const int v = min(lir + j * lpr, T.nvec - 1);
+            const uint32_t e = base + (uint32_t)(v * W);
+            gv[j] = vload32<D, W>(g, e);
+            iv[j] = vload32<uint8_t, W>(idx, e);
+            pv[j] = vload32<D, W>(p, e);
+            if (P1) vv[j] = vload32<S, W>(vm, e);
         }
+        const S mold_s = mag[rsub];
+        S vold_s = S();
+        float step_given = 0.0f;
+        if (!P1) {
+            if (T.mode == kStepsizeGiven) step_given = stepsize[rsub];
+            else vold_s = vm[rsub];
+        }
+        const float mold = to_f32(mold_s);
+        // vmean (vmean modes) or stepsize (given-stepsize mode) of the row
+        const float rowv = (T.mode == kStepsizeGiven) ? step_given : to_f32(vold_s);
         if (TAB) {
             __builtin_amdgcn_wave_barrier();
-            if (active)
-                for (int i = lir; i < 256; i += lpr) ctab[i] = L.cbd[i] * mold;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = lir + t * lpr;
+                if (i < 256) ctab[i] = L.cbd[i] * mold;
+            }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
+        float upd[R][W];
+        uint32_t mxk = 0;
+        float sumsq = 0.0f;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-            const int v = lir + j * lpr;
-            if (active && v < T.nvec) {
+            float sj = 0.0f;
 #pragma unroll
-                for (int w = 0; w < W; ++w) {
-                    const float gf = to_f32(gv[j].v[w]);
-                    const float cur = TAB ? ctab[iv[j].v[w]] : L.cbd[iv[j].v[w]] * mold;
-                    const float u = __builtin_fmaf(T.b1c, gf - cur, cur);  // lerp, weight < 0.5
-                    upd[j][w] = u;
-                    const uint32_t key = abs_key(u);
-                    mxk = key > mxk ? key : mxk;
-                    if (!P1) {
-                        const float sq = gf * gf;
-                        sumsq = sumsq + sq;
-                    }
-                }
+            for (int w = 0; w < W; ++w) {
+                const float gf = to_f32(gv[j].v[w]);
+                const float cur = TAB ? ctab[iv[j].v[w]] : L.cbd[iv[j].v[w]] * mold;
+                const float u = __builtin_fmaf(T.b1c, gf - cur, cur);  // lerp, weight < 0.5
+                upd[j][w] = u;
+                const uint32_t key = abs_key(u);
+                mxk = key > mxk ? key : mxk;
+                if (!P1) sj = __builtin_fmaf(gf, gf, sj);
             }
+            if (!P1) sumsq = sumsq + ((lir + j * lpr < T.nvec) ? sj : 0.0f);
         }
         const float mx = __uint_as_float(group_max_u32(mxk, lpr));
         float ss = 0.0f;
         if (!P1) {
             if (T.mode == kVmeanUpdate) {
                 const float tot = group_sum(sumsq, lpr);
-                if (active) {
-                    const float ms = tot / (float)T.period;
-                    const float prev = to_f32(vm[row]) * T.b2;
-                    const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, prev));
-                    if (lir == 0) vm[row] = vnew;
-                    ss = stepsize_of(to_f32(vnew), T);
-                }
+                const float ms = tot / (float)T.period;
+                const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, rowv * T.b2));
+                if (active && lir == 0) vm[rsub] = vnew;
+                ss = stepsize_of(to_f32(vnew), T);
             } else if (T.mode == kVmeanGiven) {
-                if (active) ss = stepsize_of(to_f32(vm[row]), T);
+                ss = stepsize_of(rowv, T);
             } else {
-                if (active) ss = T.stepsize[row];
+                ss = rowv;
             }
         }
-        if (!active) continue;
         const S mag_s = from_f32<S>(mx);
-        if (lir == 0) mag[row] = mag_s;
+        if (active && lir == 0) mag[rsub] = mag_s;
         const float mn = to_f32(mag_s);
         // x = upd / mn where mn > 0, else 0 (gefen.py:1184-1187).  A block whose
         // magnitude is 0, NaN or inf takes the general element path.
@@ -277,10 +291,14 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
         const bool fast = plain && two_probe;
         if (TAB && !P1) {
             if (fast) {
-                for (int i = lir; i < 256; i += lpr) {
-                    float q = L.cbd[i] * mn;
-                    if (QROUND) q = round_to<D>(q);
-                    utab[i] = (q * ss) * T.lr;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int i = lir + t * lpr;
+                    if (i < 256) {
+                        float q = L.cbd[i] * mn;
+                        if (sizeof(D) == sizeof(S)) q = round_to<D>(q);
+                        utab[i] = (q * ss) * T.lr;
+                    }
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -288,11 +306,11 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         if (fast) {
-            step_sweep2<D, S, W, R, P1, TAB, true>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, K, mn, rb,
-                                                   ss);
+            step_sweep2<D, S, W, R, P1, TAB, true>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K,
+                                                   mn, rb, ss);
         } else {
-            step_sweep2<D, S, W, R, P1, TAB, false>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, K, mn,
-                                                    rb, ss);
+            step_sweep2<D, S, W, R, P1, TAB, false>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, active,
+                                                    K, mn, rb, ss);
         }
     }
 }
