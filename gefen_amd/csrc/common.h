@@ -91,6 +91,34 @@ __device__ __forceinline__ void vstore32(T* base, uint32_t elem, const Vec<T, W>
     *reinterpret_cast<Vec<T, W>*>(reinterpret_cast<char*>(base) + off) = x;
 }
 
+// Non-temporal (streaming) variants: the data is touched once per step, so the
+// loads and stores carry the nt hint and do not displace reused lines in L2.
+template <int BYTES> struct RawVec;
+template <> struct RawVec<32> { typedef uint32_t type __attribute__((ext_vector_type(8))); };
+template <> struct RawVec<16> { typedef uint32_t type __attribute__((ext_vector_type(4))); };
+template <> struct RawVec<8> { typedef uint32_t type __attribute__((ext_vector_type(2))); };
+template <> struct RawVec<4> { typedef uint32_t type; };
+template <> struct RawVec<2> { typedef uint16_t type; };
+template <> struct RawVec<1> { typedef uint8_t type; };
+
+template <typename T, int W>
+__device__ __forceinline__ Vec<T, W> vload32_nt(const T* base, uint32_t elem) {
+    using R = typename RawVec<sizeof(T) * W>::type;
+    const uint32_t off = elem * (uint32_t)sizeof(T);
+    const R r = __builtin_nontemporal_load(reinterpret_cast<const R*>(reinterpret_cast<const char*>(base) + off));
+    Vec<T, W> x;
+    __builtin_memcpy(&x, &r, sizeof(x));
+    return x;
+}
+template <typename T, int W>
+__device__ __forceinline__ void vstore32_nt(T* base, uint32_t elem, const Vec<T, W>& x) {
+    using R = typename RawVec<sizeof(T) * W>::type;
+    const uint32_t off = elem * (uint32_t)sizeof(T);
+    R r;
+    __builtin_memcpy(&r, &x, sizeof(r));
+    __builtin_nontemporal_store(r, reinterpret_cast<R*>(reinterpret_cast<char*>(base) + off));
+}
+
 // ----------------------------------------------------------------- wave reductions
 // Butterfly over groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_max(float v, int width) {

@@ -22,8 +22,26 @@
 
 namespace gefen {
 
+#ifndef GEFEN_STEP_ITER
+#define GEFEN_STEP_ITER 4
+#endif
+#ifndef GEFEN_STEP_NT
+#define GEFEN_STEP_NT 1
+#endif
 constexpr int kThreads = 256;  // 4 waves
-constexpr int kIter = 8;       // wave-units per wave in one workgroup
+constexpr int kIter = GEFEN_STEP_ITER;  // wave-units per wave in one workgroup
+constexpr bool kStreamNT = GEFEN_STEP_NT != 0;  // non-temporal loads / stores of the streamed tensors
+
+template <typename T, int W>
+__device__ __forceinline__ Vec<T, W> sload(const T* base, uint32_t elem) {
+    if constexpr (kStreamNT) return vload32_nt<T, W>(base, elem);
+    else return vload32<T, W>(base, elem);
+}
+template <typename T, int W>
+__device__ __forceinline__ void sstore(T* base, uint32_t elem, const Vec<T, W>& x) {
+    if constexpr (kStreamNT) vstore32_nt<T, W>(base, elem, x);
+    else vstore32<T, W>(base, elem, x);
+}
 constexpr int kMaxBatch = 20;  // tasks per launch (kernel argument block < 4 KB)
 
 enum StepMode : int32_t { kVmeanUpdate = 0, kVmeanGiven = 1, kStepsizeGiven = 2 };
@@ -112,8 +130,9 @@ __device__ __forceinline__ int nearest_two_probe(float x, const float* thr, cons
 // Second sweep of a row: quantise, dequantise, update p.  FAST: the block
 // magnitude is finite and positive and the two-probe search is exact.  Every
 // lane computes all R vectors (out-of-row vectors hold a copy of the row's last
-// vector); only in-row vectors of active rows are stored.
-template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST>
+// vector); only in-row vectors of active rows are stored.  WD: weight decay
+// (gefen.py:1280-1281) is applied to the parameter first.
+template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST, bool WD>
 __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
                                             const float (&upd)[R][W], const Vec<D, W> (&gv)[R],
                                             const Vec<D, W> (&pv)[R], const Vec<S, W> (&vv)[R], uint8_t* idx, D* p,
@@ -154,15 +173,15 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
                 u = (q * s) * T.lr;
             }
             float pf = to_f32(pv[j].v[w]);
-            if (T.do_wd) pf = round_to<D>(pf * T.wdf);
+            if (WD) pf = round_to<D>(pf * T.wdf);
             po.v[w] = from_f32<D>(pf - u);
         }
         const int v = lir + j * lpr;
         if (active && v < T.nvec) {
             const uint32_t e = base + (uint32_t)(v * W);
-            vstore32<uint8_t, W>(idx, e, io);
-            vstore32<D, W>(p, e, po);
-            if (P1) vstore32<S, W>(vm, e, vo);
+            sstore<uint8_t, W>(idx, e, io);
+            sstore<D, W>(p, e, po);
+            if (P1) sstore<S, W>(vm, e, vo);
         }
     }
 }
@@ -222,10 +241,10 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
         for (int j = 0; j < R; ++j) {
             const int v = min(lir + j * lpr, T.nvec - 1);
             const uint32_t e = base + (uint32_t)(v * W);
-            gv[j] = vload32<D, W>(g, e);
-            iv[j] = vload32<uint8_t, W>(idx, e);
-            pv[j] = vload32<D, W>(p, e);
-            if (P1) vv[j] = vload32<S, W>(vm, e);
+            gv[j] = sload<D, W>(g, e);
+            iv[j] = sload<uint8_t, W>(idx, e);
+            pv[j] = sload<D, W>(p, e);
+            if (P1) vv[j] = sload<S, W>(vm, e);
         }
         const S mold_s = mag[rsub];
         S vold_s = S();
@@ -305,13 +324,17 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        if (fast) {
-            step_sweep2<D, S, W, R, P1, TAB, true>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K,
-                                                   mn, rb, ss);
+#define GEFEN_SWEEP2(FAST, WD)                                                                                 \
+    step_sweep2<D, S, W, R, P1, TAB, FAST, WD>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K, \
+                                               mn, rb, ss)
+        if (T.do_wd) {
+            if (fast) GEFEN_SWEEP2(true, true);
+            else GEFEN_SWEEP2(false, true);
         } else {
-            step_sweep2<D, S, W, R, P1, TAB, false>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, active,
-                                                    K, mn, rb, ss);
+            if (fast) GEFEN_SWEEP2(true, false);
+            else GEFEN_SWEEP2(false, false);
         }
+#undef GEFEN_SWEEP2
     }
 }
 

@@ -251,6 +251,80 @@ def _local(tensor):
     return tensor
 
 
+class _StepPlan:
+    """Cached task table of Gefen._step_all.
+
+    Valid while the optimizer's parameters with a gradient are the same objects
+    in the same order, each parameter keeps its storage, each gradient is a
+    plain contiguous tensor of the same dtype, size and device, and each
+    parameter's state tensors are the same objects.  ``refresh`` checks exactly
+    that, then advances the step counts and returns the table with the current
+    gradient addresses, hyperparameters and bias corrections; it returns None
+    (and changes nothing) when the plan no longer applies.
+    """
+
+    __slots__ = ("params", "pptr", "numel", "gdtype", "states", "srefs", "groups", "tasks", "device", "dev_index")
+
+    def __init__(self, opt, items, tasks, device):
+        self.params = [it[1] for it in items]
+        self.pptr = [it[1].data_ptr() for it in items]
+        self.numel = [it[3].numel() for it in items]
+        self.gdtype = [it[3].dtype for it in items]
+        self.states = [opt.state[it[1]] for it in items]
+        self.srefs = [(st["m_codebook"], st["m_magnitude"], st["vmean"]) for st in self.states]
+        self.groups = [it[0] for it in items]
+        self.tasks = tasks.copy()
+        self.device = device
+        self.dev_index = device.index if device.index is not None else torch.cuda.current_device()
+
+    def refresh(self, opt):
+        params, pptr, numel, gdtype = self.params, self.pptr, self.numel, self.gdtype
+        n = len(params)
+        dev = self.dev_index
+        gptr = []
+        k = 0
+        for group in opt.param_groups:
+            for p in group["params"]:
+                g = p.grad
+                if g is None:
+                    continue
+                if k == n or p is not params[k] or type(g) is not torch.Tensor:
+                    return None
+                if (g.dtype is not gdtype[k] or g.numel() != numel[k] or not g.is_contiguous()
+                        or g.get_device() != dev or p.data_ptr() != pptr[k] or not p.is_contiguous()):
+                    return None
+                gptr.append(g.data_ptr())
+                k += 1
+        if k != n:
+            return None
+        for st, (mc, mm, vm) in zip(self.states, self.srefs):
+            if st.get("m_codebook") is not mc or st.get("m_magnitude") is not mm or st.get("vmean") is not vm:
+                return None
+        lr, b1s, b2s, eps, wd, bc1, bc2 = [], [], [], [], [], [], []
+        for st, group in zip(self.states, self.groups):
+            st["step"] += 1
+            step = st["step"]
+            glr = group["lr"]
+            lr.append(float(glr.item()) if torch.is_tensor(glr) else float(glr))
+            b1, b2 = group["beta1"], group["beta2"]
+            b1s.append(b1)
+            b2s.append(b2)
+            eps.append(group["eps"])
+            wd.append(group["weight_decay"])
+            bc1.append(1 - b1 ** step)
+            bc2.append(1 - b2 ** step)
+        t = self.tasks
+        t["grad"] = gptr
+        t["lr"] = lr
+        t["beta1"] = b1s
+        t["beta2"] = b2s
+        t["eps"] = eps
+        t["weight_decay"] = wd
+        t["bias_correction_1"] = bc1
+        t["bias_correction_2"] = bc2
+        return t
+
+
 # --------------------------------------------------------------------------- optimizer
 class Gefen(torch.optim.Optimizer):
     """Gefen (gefen.py:435-1420): AdamW with an 8-bit codebook first moment and
@@ -312,6 +386,7 @@ class Gefen(torch.optim.Optimizer):
         self._exit_after_grad_sq_save = False
         self._tables = None
         self._tables_key = None
+        self._plan = None
 
         for gi, item in enumerate(params):
             if isinstance(item, dict):
@@ -620,7 +695,27 @@ class Gefen(torch.optim.Optimizer):
         return out
 
     def _step_all(self) -> None:
-        """One fused kernel pass per tensor, batched per device (gefen.py:1208-1333)."""
+        """One fused kernel pass per tensor, batched per device (gefen.py:1208-1333).
+
+        The task table is cached as a plan: while the same parameters carry
+        gradients of the same layout and the state tensors are unchanged, a step
+        only refreshes gradient addresses, step counts and hyperparameters.
+        """
+        plan = self._plan
+        tasks = plan.refresh(self) if plan is not None else None
+        if tasks is None:
+            self._plan = None
+            self._step_all_build()
+            return
+        lib = _lib.load()
+        with torch.cuda.device(plan.device):
+            rc = lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), self._codebook_tables().data_ptr(),
+                                      torch.cuda.current_stream(plan.device).cuda_stream)
+        _lib.check(rc, "gefen_step_tasks")
+
+    def _step_all_build(self) -> None:
+        """_step_all from scratch: resolves every tensor, fills the task table and,
+        when every tensor is a plain contiguous device tensor, caches the plan."""
         items = self._collect()
         if not items:
             return
@@ -633,6 +728,7 @@ class Gefen(torch.optim.Optimizer):
         tasks = np.zeros(len(items), dtype=_lib.STEP_TASK)
         keep = []
         copy_back = []
+        plain = True
         for i, (group, p, local_p, grad) in enumerate(items):
             st = self.state[p]
             period = st["automatic_period"]
@@ -641,6 +737,7 @@ class Gefen(torch.optim.Optimizer):
             lr = group["lr"]
             lr = float(lr.item()) if torch.is_tensor(lr) else float(lr)
             b1, b2 = group["beta1"], group["beta2"]
+            plain = plain and local_p is p and grad is p.grad and grad.is_contiguous()
             flat_grad = grad.reshape(-1)
             if not flat_grad.is_contiguous():
                 flat_grad = flat_grad.contiguous()
@@ -684,6 +781,8 @@ class Gefen(torch.optim.Optimizer):
         for local_p, fused_p in copy_back:
             local_p.copy_(fused_p)
         del keep
+        if plain and all(it[3].device == dev for it in items):
+            self._plan = _StepPlan(self, items, tasks, dev)
 
     def _optimizer_state_memory_bytes(self) -> int:
         return sum(v.numel() * v.element_size() for s in self.state.values() for v in s.values() if torch.is_tensor(v))
@@ -704,6 +803,7 @@ class Gefen(torch.optim.Optimizer):
         saved = state_dict.get("state", {}) or {}
         codebook = state_dict.pop("gefen_codebook", None)
         super().load_state_dict(state_dict)
+        self._plan = None
         self._gefen_global_step = gstep
         if self._cap_period_by_shape_enabled():
             for group in self.param_groups:

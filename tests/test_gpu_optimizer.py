@@ -158,3 +158,52 @@ def test_gefen_muon_matches_reference_trajectory(name):
                 tol = 0.05 if dtype != "f32" else 0.03
                 rel = np.linalg.norm(ours - ref) / max(np.linalg.norm(ref), 1e-30)
                 assert rel <= tol, "{} p{} step {}: relative update error {:.3g}".format(name, i, step, rel)
+
+
+def test_cached_step_plan_matches_rebuilt_task_table():
+    """Steps through the cached plan equal steps that rebuild the task table from
+    scratch, bit for bit, across the events that invalidate the plan: an lr
+    change, a skipped gradient, a non-contiguous gradient, load_state_dict and
+    a weight-decay change."""
+    from gefen_amd.gefen import Gefen
+
+    shapes = [(64, 96), (96,), (32, 48), (128, 256)]
+
+    def make():
+        gen = torch.Generator().manual_seed(1)
+        return [(torch.randn(s, generator=gen) * 0.02).to(torch.bfloat16).to("cuda:0").requires_grad_(True)
+                for s in shapes]
+
+    pa, pb = make(), make()
+    oa = Gefen([("t{}".format(i), t) for i, t in enumerate(pa)])
+    ob = Gefen([("t{}".format(i), t) for i, t in enumerate(pb)])
+    gen = torch.Generator().manual_seed(2)
+    planned = 0
+    for step in range(1, 13):
+        if step == 4:
+            oa.param_groups[0]["lr"] = ob.param_groups[0]["lr"] = 2e-3
+        if step == 10:
+            oa.param_groups[3]["weight_decay"] = ob.param_groups[3]["weight_decay"] = 0.1
+        if step == 9:
+            oa.load_state_dict(copy.deepcopy(oa.state_dict()))
+            ob.load_state_dict(copy.deepcopy(ob.state_dict()))
+        for i, s in enumerate(shapes):
+            g = (torch.randn(s, generator=gen) * 1e-3).to(torch.bfloat16).to("cuda:0")
+            if step == 5 and i == 1:
+                g = None
+            elif step == 7 and i == 2:
+                g = g.t().contiguous().t()  # same values, transposed strides
+            pa[i].grad = g
+            pb[i].grad = None if g is None else g.clone()
+        planned += oa._plan is not None
+        ob._plan = None
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for i in range(len(shapes)):
+            np.testing.assert_array_equal(gu.to_np(pa[i]), gu.to_np(pb[i]), err_msg="step {} p{}".format(step, i))
+            for key in ("m_codebook", "m_magnitude", "vmean"):
+                np.testing.assert_array_equal(gu.to_np(oa.state[pa[i]][key]), gu.to_np(ob.state[pb[i]][key]),
+                                              err_msg="step {} {} {}".format(step, key, i))
+            assert oa.state[pa[i]]["step"] == ob.state[pb[i]]["step"]
+    assert planned >= 6  # the plan served most steps
