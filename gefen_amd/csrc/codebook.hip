@@ -70,8 +70,10 @@ __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restric
             c = (uint16_t)(lo - 1);
         }
         T->bucket[e] = c;
+        T->bucket8[e] = (uint8_t)c;  // c <= K - 1 <= 255
         bk[e] = c;
     }
+    if (t < 12) T->bucket8[4100 + t] = 0;
     if (t == 0) probe_max = 0;
     __syncthreads();
     // a search from bucket b (one below x's bucket) meets the thresholds in

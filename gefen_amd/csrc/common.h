@@ -141,9 +141,12 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 //   max_probe: most thresholds a search started one bucket low can meet before
 //            reaching x (0 if thresholds lie below -1); <= 2 lets the kernels
 //            use the fixed two-probe search.
+//   bucket8  the same counts as bytes (every count is <= 255), padded with zeros
+//            to 4112 entries: the compact copy the step kernels keep in LDS.
 struct CodebookTables {
     float cb[256];
     float thr[260];
+    uint8_t bucket8[4112];
     uint16_t bucket[4100];
     int32_t K;
     int32_t max_probe;
@@ -191,7 +194,8 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t v, int width) {
 // case.  The bucket is taken one below floor((x + 1) * 2048) so that the fma's
 // rounding can only move it down; its count of thresholds < edge is <= the
 // answer, and the remaining thresholds in [edge, x) are counted by probing.
-__device__ __forceinline__ int nearest_fast(float x, const float* thr, const uint16_t* bucket, int K) {
+template <typename B>
+__device__ __forceinline__ int nearest_fast(float x, const float* thr, const B* bucket, int K) {
     float y = __builtin_fmaf(x, 2048.0f, 2048.0f);
     y = fminf(fmaxf(y, 1.0f), 4097.0f);
     const int b = (int)y - 1;

@@ -12,6 +12,7 @@
 // The arithmetic is the reference's CPU path (gefen.py:116-119, 1153-1206,
 // 1280-1281, 1326-1333; gefen_muon.py:132-171, 302-316), op by op.
 #include <math.h>
+#include <stddef.h>
 #include <string.h>
 
 #include <algorithm>
@@ -25,11 +26,27 @@ namespace gefen {
 #ifndef GEFEN_STEP_ITER
 #define GEFEN_STEP_ITER 4
 #endif
+#ifndef GEFEN_STEP_ITER_ROWS
+#define GEFEN_STEP_ITER_ROWS 1
+#endif
+#ifndef GEFEN_STEP_ITER_P1
+#define GEFEN_STEP_ITER_P1 2
+#endif
 #ifndef GEFEN_STEP_NT
 #define GEFEN_STEP_NT 1
 #endif
-constexpr int kThreads = 256;  // 4 waves
-constexpr int kIter = GEFEN_STEP_ITER;  // wave-units per wave in one workgroup
+#ifndef GEFEN_STEP_WAVES
+#define GEFEN_STEP_WAVES 4
+#endif
+constexpr int kThreads = 256;  // 4 waves: two-sweep, GefenMuon and vmean kernels
+constexpr int kIter = GEFEN_STEP_ITER;  // wave-units per wave in one GefenMuon workgroup
+// wave-units per wave in one step workgroup: block rows, period-one rows
+constexpr int kIterRows = GEFEN_STEP_ITER_ROWS;
+constexpr int kIterP1 = GEFEN_STEP_ITER_P1;
+template <bool P1> constexpr int step_iter() { return P1 ? kIterP1 : kIterRows; }
+constexpr int kStepWaves = GEFEN_STEP_WAVES;  // waves per workgroup of the register-path step kernel
+constexpr int kStepThreads = 64 * kStepWaves;
+
 constexpr bool kStreamNT = GEFEN_STEP_NT != 0;  // non-temporal loads / stores of the streamed tensors
 
 template <typename T, int W>
@@ -73,21 +90,49 @@ struct StepBatch {
     const CodebookTables* tables;
 };
 
-// LDS copy of the codebook tables, with the codebook rounded to the parameter dtype.
-struct LdsTables {
-    float cbd[256];
+// LDS copy of the codebook tables (6 KB): the codebook rounded to the parameter
+// dtype, the thresholds and the byte bucket index.
+struct alignas(16) LdsTables {
     float thr[260];
-    uint16_t bucket[4100];
+    uint8_t bucket[4112];
+    float cbd[256];
 };
+static_assert(offsetof(CodebookTables, thr) % 16 == 0 && offsetof(CodebookTables, bucket8) % 16 == 0,
+              "codebook tables must allow 16-byte copies");
 
-template <typename D>
+// The LDS tables are 386 16-byte pieces: thr and bucket8 follow each other in
+// CodebookTables (pieces 64..385 there), the codebook is pieces 0..63.  Every
+// piece of a thread is loaded before any is stored, so a workgroup waits for
+// one round trip to L2, not one per table.
+static_assert(offsetof(CodebookTables, thr) == 1024 && offsetof(CodebookTables, bucket8) == 2064 &&
+                  sizeof(LdsTables) == 386 * 16 && offsetof(LdsTables, bucket) == 65 * 16 &&
+                  offsetof(LdsTables, cbd) == 322 * 16,
+              "table layout");
+
+template <typename D, int NT>
 __device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* T, int& K) {
+    using U4 = RawVec<16>::type;
+    constexpr int kPieces = 386, kPer = (kPieces + NT - 1) / NT;
     K = T->K;
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) L.cbd[i] = round_to<D>(T->cb[i]);
-    for (int i = threadIdx.x; i < 260; i += blockDim.x) L.thr[i] = T->thr[i];
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(T->bucket);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(L.bucket);
-    for (int i = threadIdx.x; i < 2050; i += blockDim.x) dst[i] = src[i];
+    const U4* src = reinterpret_cast<const U4*>(T);
+    U4* dst = reinterpret_cast<U4*>(&L);
+    U4 v[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int q = threadIdx.x + r * NT;
+        if (q < kPieces) v[r] = src[q < 322 ? q + 64 : q - 322];
+    }
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int q = threadIdx.x + r * NT;
+        if (q < kPieces) {
+            if (q >= 322) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[r][c] = __float_as_uint(round_to<D>(__uint_as_float(v[r][c])));
+            }
+            dst[q] = v[r];
+        }
+    }
     __syncthreads();
 }
 
@@ -118,7 +163,7 @@ __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
 
 // Nearest index with at most two threshold probes (max_probe <= 2): one
 // ds_read2 of thr[k+1], thr[k+2] after the bucket lookup.
-__device__ __forceinline__ int nearest_two_probe(float x, const float* thr, const uint16_t* bucket) {
+__device__ __forceinline__ int nearest_two_probe(float x, const float* thr, const uint8_t* bucket) {
     float y = __builtin_fmaf(x, 2048.0f, 2047.0f);  // (x + 1) * 2048 - 1, rounded once
     y = fminf(fmaxf(y, 0.0f), 4096.0f);
     int k = bucket[(int)y];
@@ -132,9 +177,9 @@ __device__ __forceinline__ int nearest_two_probe(float x, const float* thr, cons
 // lane computes all R vectors (out-of-row vectors hold a copy of the row's last
 // vector); only in-row vectors of active rows are stored.  WD: weight decay
 // (gefen.py:1280-1281) is applied to the parameter first.
-template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST, bool WD>
+template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST, bool WD, typename UF>
 __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
-                                            const float (&upd)[R][W], const Vec<D, W> (&gv)[R],
+                                            const UF& upd_of, const Vec<D, W> (&gv)[R],
                                             const Vec<D, W> (&pv)[R], const Vec<S, W> (&vv)[R], uint8_t* idx, D* p,
                                             S* vm, uint32_t base, int lir, int lpr, bool active, int K, float mn,
                                             double rb, float ss) {
@@ -148,10 +193,11 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
         for (int w = 0; w < W; ++w) {
             int k;
             if (FAST) {
-                k = nearest_two_probe(div_by_block(upd[j][w], rb), L.thr, L.bucket);
+                k = nearest_two_probe(div_by_block(upd_of(j, w), rb), L.thr, L.bucket);
             } else {
                 const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
-                const float x = plain ? div_by_block(upd[j][w], rb) : ((mn > 0.0f) ? upd[j][w] / mn : 0.0f);
+                const float uj = upd_of(j, w);
+                const float x = plain ? div_by_block(uj, rb) : ((mn > 0.0f) ? uj / mn : 0.0f);
                 k = nearest_fast(x, L.thr, L.bucket, K);
             }
             io.v[w] = (uint8_t)k;
@@ -196,11 +242,11 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
 // so each lane has all of its row's bytes in flight at once.  Absmax is
 // idempotent under such copies; the sum of squares masks them out.
 template <typename D, typename S, int W, int R, bool P1, bool TAB>
-__global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
+__global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) {
     __shared__ LdsTables L;
-    __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
+    __shared__ float row_tab[TAB ? kStepWaves : 1][TAB ? 2 : 1][2][256];
     int K;
-    load_tables<D>(L, B.tables, K);
+    load_tables<D, kStepThreads>(L, B.tables, K);
     const bool two_probe = B.tables->max_probe <= 2;
     const int ti = find_task(B.wg_begin, B.ntasks);
     const StepTask T = B.t[ti];
@@ -215,8 +261,9 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
     float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
     float* utab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
 
-    for (int it = 0; it < kIter; ++it) {
-        const int64_t unit = (lw * kIter + it) * 4 + wave;
+    constexpr int kIt = step_iter<P1>();
+    for (int it = 0; it < kIt; ++it) {
+        const int64_t unit = (lw * kIt + it) * kStepWaves + wave;
         const int64_t row0 = unit * rpw;
         if (row0 >= T.nrows) break;  // uniform across the wave
         const int64_t row = row0 + sub;
@@ -303,6 +350,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
         const S mag_s = from_f32<S>(mx);
         if (active && lir == 0) mag[rsub] = mag_s;
         const float mn = to_f32(mag_s);
+        auto upd_of = [&](int j, int w) -> float { return upd[j][w]; };
         // x = upd / mn where mn > 0, else 0 (gefen.py:1184-1187).  A block whose
         // magnitude is 0, NaN or inf takes the general element path.
         const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
@@ -325,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step(const StepBatch B) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
 #define GEFEN_SWEEP2(FAST, WD)                                                                                 \
-    step_sweep2<D, S, W, R, P1, TAB, FAST, WD>(T, L, utab, upd, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K, \
+    step_sweep2<D, S, W, R, P1, TAB, FAST, WD>(T, L, utab, upd_of, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K, \
                                                mn, rb, ss)
         if (T.do_wd) {
             if (fast) GEFEN_SWEEP2(true, true);
@@ -346,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step_long(const StepBatch B)
     __shared__ LdsTables L;
     __shared__ float red_mx[4], red_sum[4];
     int K;
-    load_tables<D>(L, B.tables, K);
+    load_tables<D, kThreads>(L, B.tables, K);
     const int ti = find_task(B.wg_begin, B.ntasks);
     const StepTask& T = B.t[ti];
     constexpr bool QROUND = sizeof(D) == sizeof(S);
@@ -448,7 +496,7 @@ template <typename D, typename S, int W, int R>
 __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     __shared__ LdsTables L;
     int K;
-    load_tables<D>(L, B.tables, K);
+    load_tables<D, kThreads>(L, B.tables, K);
     const int ti = find_task(B.wg_begin, B.ntasks);
     const MuonTask& T = B.t[ti];
     const int lane = threadIdx.x & 63;
@@ -531,7 +579,7 @@ __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
     __shared__ LdsTables L;
     __shared__ float red_mx[4];
     int K;
-    load_tables<D>(L, B.tables, K);
+    load_tables<D, kThreads>(L, B.tables, K);
     const int ti = find_task(B.wg_begin, B.ntasks);
     const MuonTask& T = B.t[ti];
     const int64_t row = blockIdx.x - B.wg_begin[ti];
@@ -665,10 +713,10 @@ hipError_t launch_step(const Key& k, const StepBatch& b, int grid, hipStream_t s
 #define GEFEN_STEP_CASE(WW, RR)                                                                          \
     if (k.W == WW && k.R == RR) {                                                                       \
         if (k.p1) {                                                                                     \
-            hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, true, false>), dim3(grid), dim3(kThreads), 0, st, b);           \
+            hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, true, false>), dim3(grid), dim3(kStepThreads), 0, st, b);           \
         } else {                                                                                        \
-            if (k.tab) hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false, true>), dim3(grid), dim3(kThreads), 0, st, b); \
-            else hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false, false>), dim3(grid), dim3(kThreads), 0, st, b);      \
+            if (k.tab) hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false, true>), dim3(grid), dim3(kStepThreads), 0, st, b); \
+            else hipLaunchKernelGGL((k_gefen_step<D, S, WW, RR, false, false>), dim3(grid), dim3(kStepThreads), 0, st, b);      \
         }                                                                                               \
         return hipGetLastError();                                                                       \
     }
@@ -730,11 +778,11 @@ hipError_t dispatch_muon(const Key& k, const MuonBatch& b, int grid, hipStream_t
 bool valid_pair(int d, int s) { return valid_dtype(d) && valid_dtype(s) && (d == s || s == GEFEN_F32); }
 
 // Work of one task in workgroups for its kernel key.
-int32_t task_wgs(const Key& k, int64_t nrows, int lpr_log2) {
+int32_t task_wgs(const Key& k, int64_t nrows, int lpr_log2, int waves, int iters) {
     if (k.R == 0) return (int32_t)nrows;
     const int64_t rpw = 64 >> lpr_log2;
     const int64_t units = (nrows + rpw - 1) / rpw;
-    return (int32_t)((units + 4 * kIter - 1) / (4 * kIter));
+    return (int32_t)((units + waves * iters - 1) / (waves * iters));
 }
 
 struct PendingStep {
@@ -815,7 +863,7 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     t.lr = (float)in.lr;
     t.do_wd = in.weight_decay > 0.0;
     t.wdf = (float)(1.0 - in.lr * in.weight_decay);
-    t.nwg = task_wgs(k, t.nrows, l2);
+    t.nwg = task_wgs(k, t.nrows, l2, kStepWaves, k.p1 ? kIterP1 : kIterRows);
     out.key = k;
     return GEFEN_OK;
 }
@@ -1069,7 +1117,7 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     t.alpha = round_host(alpha, in.grad_dtype);
     t.tiny = round_host(tiny, in.state_dtype);
     t.nesterov = in.nesterov ? 1 : 0;
-    t.nwg = task_wgs(k, t.nrows, l2);
+    t.nwg = task_wgs(k, t.nrows, l2, 4, kIter);
     out.key = k;
     return GEFEN_OK;
 }
