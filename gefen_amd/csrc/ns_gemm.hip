@@ -24,6 +24,7 @@ namespace ns {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int LDK = BK + 8;  // padded LDS row (bf16 elements): 80 bytes
@@ -183,6 +184,164 @@ __global__ __launch_bounds__(NT) void k_gemm(const uint16_t* __restrict__ A, int
             }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile batched GEMM for the Newton-Schulz products, all in "A B^T" form:
+//
+//   C_b = alpha * A_b @ B_b^T + beta * D_b     (bf16 out, one rounding)
+//
+// A_b [M, K] and B_b [N, K] are row-major, so both operands are K-contiguous
+// (the Gram matrix X X^T, A A with A symmetric, and B X with X^T kept beside X).
+// A 512-thread workgroup owns a 256x256 tile; its eight waves (2 x 4) each own
+// 128x64 as 4x2 v_mfma_f32_32x32x16_bf16 tiles (128 fp32 accumulators per
+// lane).  K moves
+// 32 at a time: two register stages and two LDS stages give a prefetch distance
+// of two steps.  Symmetric outputs (X X^T, b A + c A A) compute only the tiles
+// on and above the diagonal and mirror them; CT (optional) receives C^T.
+// M and N must be multiples of 256, K a multiple of 32, every row 16-byte
+// aligned; other shapes take k_gemm.
+constexpr int TM = 256, TN = 256, TK = 32;
+constexpr int TLD = TK + 8;  // LDS row: 40 bf16 = 80 bytes
+constexpr int TT = 512;
+constexpr int WI = 4, WJ = 2;  // 32x32 MFMA tiles per wave (rows, columns)
+constexpr int TCH = TM * TK / 8 / TT;  // 16-byte chunks per thread per operand tile
+
+struct TileGemm {
+    const uint16_t* A;
+    const uint16_t* B;
+    uint16_t* C;
+    uint16_t* CT;
+    const uint16_t* D;
+    int64_t lda, ldb, ldc, ldct, ldd;
+    int64_t sa, sb, sc, sct, sd;  // batch strides (elements)
+    int M, N, K;
+    float alpha, beta;
+    int tiles_n;   // N / TN
+    int tiles;     // tiles per matrix
+    int symmetric;
+};
+
+// The TCH 16-byte chunks of this thread in a 256 x 32 operand tile: chunk q =
+// threadIdx.x + TT i is row q / 4, k-chunk q % 4.
+__device__ __forceinline__ void tile_load(const uint16_t* __restrict__ src, int64_t ld, int r0, int k0,
+                                          u32x4 out[TCH]) {
+#pragma unroll
+    for (int i = 0; i < TCH; ++i) {
+        const int q = threadIdx.x + TT * i;
+        out[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + (q >> 2)) * ld + k0 + (q & 3) * 8);
+    }
+}
+__device__ __forceinline__ void tile_store(uint16_t* lds, const u32x4 in[TCH]) {
+#pragma unroll
+    for (int i = 0; i < TCH; ++i) {
+        const int q = threadIdx.x + TT * i;
+        *reinterpret_cast<u32x4*>(lds + (q >> 2) * TLD + (q & 3) * 8) = in[i];
+    }
+}
+
+__global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * TLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][TN * TLD];
+    const int batch = blockIdx.x / g.tiles;
+    int t = blockIdx.x - batch * g.tiles;
+    int ti, tj;
+    if (g.symmetric) {  // tiles (ti, tj), ti <= tj, row by row
+        ti = 0;
+        while (t >= g.tiles_n - ti) {
+            t -= g.tiles_n - ti;
+            ++ti;
+        }
+        tj = ti + t;
+    } else {
+        ti = t / g.tiles_n;
+        tj = t - ti * g.tiles_n;
+    }
+    const int m0 = ti * TM, n0 = tj * TN;
+    const uint16_t* __restrict__ A = g.A + batch * g.sa;
+    const uint16_t* __restrict__ B = g.B + batch * g.sb;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 2) * (32 * WI), wn = (wave & 3) * (32 * WJ);
+    f32x16 acc[WI][WJ];
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int nk = g.K / TK;
+    u32x4 ra0[TCH], rb0[TCH], ra1[TCH], rb1[TCH];  // register stages 0 and 1
+    tile_load(A, g.lda, m0, 0, ra0);
+    tile_load(B, g.ldb, n0, 0, rb0);
+    if (nk > 1) {
+        tile_load(A, g.lda, m0, TK, ra1);
+        tile_load(B, g.ldb, n0, TK, rb1);
+    }
+    tile_store(As[0], ra0);
+    tile_store(Bs[0], rb0);
+    __syncthreads();
+    // one K step from LDS stage CUR; register stage CUR refills with step kt + 2
+#define GEFEN_TILE_STEP(KT, CUR, RA, RB, RA_NEXT, RB_NEXT)                                                       \
+    {                                                                                                             \
+        if ((KT) + 2 < nk) { /* register stage CUR was stored to LDS already */                                   \
+            tile_load(A, g.lda, m0, ((KT) + 2) * TK, RA);                                                         \
+            tile_load(B, g.ldb, n0, ((KT) + 2) * TK, RB);                                                         \
+        }                                                                                                         \
+        const uint16_t* as = As[CUR];                                                                             \
+        const uint16_t* bs = Bs[CUR];                                                                             \
+        _Pragma("unroll") for (int kk = 0; kk < TK; kk += 16) {                                                   \
+            bf16x8 af[WI], bfr[WJ];                                                                               \
+            _Pragma("unroll") for (int i = 0; i < WI; ++i) af[i] =                                                \
+                *reinterpret_cast<const bf16x8*>(as + (wm + i * 32 + (lane & 31)) * TLD + kk + 8 * (lane >> 5));  \
+            _Pragma("unroll") for (int j = 0; j < WJ; ++j) bfr[j] =                                               \
+                *reinterpret_cast<const bf16x8*>(bs + (wn + j * 32 + (lane & 31)) * TLD + kk + 8 * (lane >> 5));  \
+            _Pragma("unroll") for (int i = 0; i < WI; ++i) _Pragma("unroll") for (int j = 0; j < WJ; ++j)          \
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);           \
+        }                                                                                                         \
+        if ((KT) + 1 < nk) {                                                                                      \
+            tile_store(As[(CUR) ^ 1], RA_NEXT);                                                                   \
+            tile_store(Bs[(CUR) ^ 1], RB_NEXT);                                                                   \
+        }                                                                                                         \
+        __syncthreads();                                                                                          \
+    }
+    for (int kt = 0; kt < nk; kt += 2) {
+        GEFEN_TILE_STEP(kt, 0, ra0, rb0, ra1, rb1)
+        if (kt + 1 < nk) GEFEN_TILE_STEP(kt + 1, 1, ra1, rb1, ra0, rb0)
+    }
+#undef GEFEN_TILE_STEP
+    // epilogue: C = alpha * acc + beta * D rounded once; four consecutive rows of
+    // one column go to CT (and to the mirror tile) as one 8-byte store
+    uint16_t* __restrict__ C = g.C + batch * g.sc;
+    uint16_t* __restrict__ CT = g.CT ? g.CT + batch * g.sct : nullptr;
+    const uint16_t* __restrict__ D = g.D ? g.D + batch * g.sd : nullptr;
+    const bool mirror = g.symmetric && ti != tj;
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int col = n0 + wn + j * 32 + (lane & 31);
+                const int row0 = m0 + wm + i * 32 + 8 * r4 + 4 * (lane >> 5);
+                uint16_t o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = row0 + r;
+                    float v = g.alpha * acc[i][j][4 * r4 + r];
+                    if (D) {
+                        const float d = __uint_as_float((uint32_t)D[(int64_t)row * g.ldd + col] << 16);
+                        v = v + g.beta * d;
+                    }
+                    o[r] = from_f32<bf16_t>(v).bits;
+                    C[(int64_t)row * g.ldc + col] = o[r];
+                }
+                uint2 packed;
+                packed.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+                packed.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+                if (CT) *reinterpret_cast<uint2*>(CT + (int64_t)col * g.ldct + row0) = packed;
+                if (mirror) *reinterpret_cast<uint2*>(C + (int64_t)col * g.ldc + row0) = packed;
+            }
+}
+
 }  // namespace ns
 }  // namespace gefen
 
@@ -211,4 +370,46 @@ extern "C" int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_
         hipLaunchKernelGGL(ns::k_gemm<false>, grid, dim3(ns::NT), 0, st, A, lda, B, ldb, C, ldc, D, ldd, m, n, k,
                            (float)alpha, (float)beta, vec_a, vec_b);
     return launch_status("gefen_gemm_bf16");
+}
+
+extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
+                                          int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, void* ct,
+                                          int64_t ldct, int64_t stride_ct, const void* d, int64_t ldd,
+                                          int64_t stride_d, int batch, int m, int n, int k, double alpha,
+                                          double beta, int symmetric, gefen_stream_t stream) {
+    if (m < 0 || n < 0 || k < 0 || batch < 0) return fail_inval("negative GEMM size");
+    if (m == 0 || n == 0 || batch == 0) return GEFEN_OK;
+    if (!a || !b || !c || (beta != 0.0 && !d)) return fail_inval("null GEMM operand");
+    if (lda < k || ldb < k || ldc < n || (ct && ldct < m) || (d && ldd < n))
+        return fail_inval("GEMM leading dimension too small");
+    if (symmetric && m != n) return fail_inval("a symmetric GEMM must be square");
+    if (symmetric && ct) return fail_inval("a symmetric GEMM has no separate transposed output (C^T = C)");
+    if (m % ns::TM || n % ns::TN || k % ns::TK || k == 0)
+        return fail_inval("batched GEMM needs M, N multiples of 256 and K a multiple of 32 (got %d, %d, %d)", m, n, k);
+    const void* ptrs[5] = {a, b, c, ct, d};
+    const int64_t lds_[5] = {lda, ldb, ldc, ldct, ldd};
+    const int64_t strides[5] = {stride_a, stride_b, stride_c, stride_ct, stride_d};
+    for (int i = 0; i < 5; ++i) {
+        if (!ptrs[i]) continue;
+        if (!aligned(ptrs[i], 16) || lds_[i] % 8 || strides[i] % 8)
+            return fail_inval("batched GEMM operands need 16-byte aligned rows");
+    }
+    ns::TileGemm g;
+    g.A = static_cast<const uint16_t*>(a);
+    g.B = static_cast<const uint16_t*>(b);
+    g.C = static_cast<uint16_t*>(c);
+    g.CT = static_cast<uint16_t*>(ct);
+    g.D = beta != 0.0 ? static_cast<const uint16_t*>(d) : nullptr;
+    g.lda = lda; g.ldb = ldb; g.ldc = ldc; g.ldct = ldct; g.ldd = ldd;
+    g.sa = stride_a; g.sb = stride_b; g.sc = stride_c; g.sct = stride_ct; g.sd = stride_d;
+    g.M = m; g.N = n; g.K = k;
+    g.alpha = (float)alpha;
+    g.beta = (float)beta;
+    g.tiles_n = n / ns::TN;
+    g.symmetric = symmetric ? 1 : 0;
+    g.tiles = symmetric ? g.tiles_n * (g.tiles_n + 1) / 2 : (m / ns::TM) * g.tiles_n;
+    const int64_t grid = (int64_t)g.tiles * batch;
+    if (grid > INT32_MAX) return fail_inval("batched GEMM grid too large");
+    hipLaunchKernelGGL(ns::k_gemm_tile, dim3((unsigned)grid), dim3(ns::TT), 0, reinterpret_cast<hipStream_t>(stream), g);
+    return launch_status("gefen_gemm_bf16_nt_batched");
 }

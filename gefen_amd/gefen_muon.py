@@ -26,6 +26,14 @@ DEFAULT_C = 2.0315
 DEFAULT_NS_STEPS = 5
 
 
+def _check_ns_args(ns_coefficients, ns_steps: int) -> None:
+    """The argument checks of gefen_muon.py:23-30."""
+    if ns_steps >= 100:
+        raise ValueError("Number of steps must be less than 100 for computational efficiency")
+    if len(ns_coefficients) != 3:
+        raise ValueError("Coefficients must be a tuple of exactly 3 values")
+
+
 def _zeropower_via_newtonschulz(grad: torch.Tensor, ns_coefficients: Tuple[float, float, float], ns_steps: int,
                                 eps: float) -> torch.Tensor:
     """Quintic Newton-Schulz iteration in bf16 (gefen_muon.py:16-51)."""
@@ -158,6 +166,24 @@ class GefenMuon(Gefen):
             raise ValueError("Expected Gefen codebook to be initialized before fused GefenMuon update.")
         tables = self._codebook_tables()
         tasks = np.zeros(len(items), dtype=_lib.MUON_TASK)
+        # Matrices of one shape, dtype and Newton-Schulz setting share a stacked
+        # buffer: the momentum kernel writes each one's Nesterov blend into its
+        # slice and Newton-Schulz runs on the whole stack.
+        from gefen_amd.newton_schulz import batched_shape_ok
+
+        stacks = {}
+        for i, (group, p, local_p, grad) in enumerate(items):
+            rows, cols = grad.shape
+            if batched_shape_ok(rows, cols):
+                key = (rows, cols, grad.dtype, tuple(group["ns_coefficients"]), group["ns_steps"], group["eps"])
+                stacks.setdefault(key, []).append(i)
+        where = {}
+        bufs = {}
+        for key, idx in stacks.items():
+            rows, cols, dtype = key[0], key[1], key[2]
+            bufs[key] = torch.empty(len(idx), rows, cols, dtype=dtype, device=items[idx[0]][3].device)
+            for slot, i in enumerate(idx):
+                where[i] = (key, slot)
         outs = []
         keep = []
         for i, (group, p, local_p, grad) in enumerate(items):
@@ -167,7 +193,11 @@ class GefenMuon(Gefen):
             if not flat.is_contiguous():
                 flat = flat.contiguous()
             keep.append(flat)
-            out = torch.empty_like(flat)
+            if i in where:
+                key, slot = where[i]
+                out = bufs[key][slot].view(-1)
+            else:
+                out = torch.empty_like(flat)
             outs.append(out)
             t = tasks[i]
             t["grad"] = flat.data_ptr()
@@ -186,11 +216,24 @@ class GefenMuon(Gefen):
             rc = lib.gefen_muon_tasks(tasks.ctypes.data, len(items), tables.data_ptr(),
                                       torch.cuda.current_stream(dev).cuda_stream)
         _lib.check(rc, "gefen_muon_tasks")
-        for (group, p, local_p, grad), out in zip(items, outs):
+        updates = {}
+        if stacks:
+            from gefen_amd.newton_schulz import newton_schulz_batched
+
+            for key, idx in stacks.items():
+                coeffs, steps, eps = key[3], key[4], key[5]
+                _check_ns_args(coeffs, steps)
+                x = bufs[key] if key[2] == torch.bfloat16 else bufs[key].bfloat16()
+                res = newton_schulz_batched(x, coeffs, steps, eps)
+                for slot, i in enumerate(idx):
+                    updates[i] = res[slot]
+        for i, ((group, p, local_p, grad), out) in enumerate(zip(items, outs)):
             st = self.state[p]
             st["step"] += 1
-            update = _zeropower_via_newtonschulz(out.view_as(grad), group["ns_coefficients"], group["ns_steps"],
-                                                 group["eps"])
+            update = updates.get(i)
+            if update is None:
+                update = _zeropower_via_newtonschulz(out.view_as(grad), group["ns_coefficients"], group["ns_steps"],
+                                                     group["eps"])
             lr = group["lr"]
             lr = float(lr.item()) if torch.is_tensor(lr) else float(lr)
             adjusted = _adjust_lr(lr, group["adjust_lr_fn"], p.shape)

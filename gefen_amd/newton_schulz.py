@@ -1,8 +1,13 @@
 """Newton-Schulz orthogonalisation of GefenMuon (gefen_muon.py:16-51) on MFMA.
 
 X = bf16(G) (transposed when rows > cols), X /= max(||X||, eps), then ns_steps
-times:  A = X X^T;  B = b A + c A A;  X = a X + B X.  Each product is one
-gefen_gemm_bf16 call (fp32 accumulation, one bf16 rounding of alpha*AB + beta*D).
+times:  A = X X^T;  B = b A + c A A;  X = a X + B X.  Each product rounds
+alpha*AB + beta*D to bf16 once, as torch.addmm does.
+
+newton_schulz_batched runs a stack of same-shaped matrices at once with the
+large-tile batched GEMM (every product in A B^T form: X X^T, A A with A
+symmetric, B X from X^T, which each step writes beside X); newton_schulz_bf16
+is the one-matrix path for shapes the batched GEMM does not tile.
 """
 
 from __future__ import annotations
@@ -49,3 +54,60 @@ def newton_schulz_bf16(grad: torch.Tensor, coeffs: Tuple[float, float, float], s
     if transposed:
         x = x.T
     return x
+
+
+def batched_shape_ok(rows: int, cols: int) -> bool:
+    """The batched GEMM tiles m = min(rows, cols) and n = max(rows, cols) by 256."""
+    return rows > 0 and cols > 0 and rows % 256 == 0 and cols % 256 == 0
+
+
+def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: torch.Tensor = None,
+                    d: torch.Tensor = None, alpha: float = 1.0, beta: float = 0.0, symmetric: bool = False) -> None:
+    """out[i] = alpha * a[i] @ b[i]^T + beta * d[i] (and out_t[i] = out[i]^T) for stacked bf16 matrices."""
+    g, m, k = a.shape
+    n = b.shape[1]
+    lib = _lib.load()
+
+    def ptr(t):
+        return t.data_ptr() if t is not None else None
+
+    def ld(t):
+        return t.stride(1) if t is not None else 0
+
+    def bs(t):
+        return t.stride(0) if t is not None else 0
+
+    rc = lib.gefen_gemm_bf16_nt_batched(a.data_ptr(), a.stride(1), a.stride(0), b.data_ptr(), b.stride(1), b.stride(0),
+                                        out.data_ptr(), out.stride(1), out.stride(0), ptr(out_t), ld(out_t), bs(out_t),
+                                        ptr(d), ld(d), bs(d), g, m, n, k, float(alpha), float(beta),
+                                        1 if symmetric else 0, torch.cuda.current_stream(a.device).cuda_stream)
+    _lib.check(rc, "gefen_gemm_bf16_nt_batched")
+
+
+def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], steps: int,
+                          eps: float) -> torch.Tensor:
+    """Newton-Schulz of every matrix of a [G, rows, cols] bf16 stack, in place of
+    x's values (x is normalised in place); returns the [G, rows, cols] result."""
+    a, b, c = coeffs
+    g, rows, cols = x.shape
+    transposed = rows > cols
+    # normalise each matrix: x /= max(||x||, eps) in bf16 (gefen_muon.py:37)
+    nrm = torch.linalg.vector_norm(x.view(g, -1), dim=1).clamp(min=eps)
+    x.div_(nrm.view(g, 1, 1))
+    # X [G, m, n] with m <= n and its transpose
+    if transposed:
+        xt, x = x, x.transpose(1, 2).contiguous()
+    else:
+        xt = x.transpose(1, 2).contiguous()
+    m, n = x.shape[1], x.shape[2]
+    gram = torch.empty(g, m, m, dtype=torch.bfloat16, device=x.device)
+    upd = torch.empty_like(gram)
+    nx, nxt = torch.empty_like(x), torch.empty_like(xt)
+    with torch.cuda.device(x.device):
+        for _ in range(steps):
+            gemm_nt_batched(x, x, gram, symmetric=True)                                # X X^T
+            gemm_nt_batched(gram, gram, upd, d=gram, alpha=c, beta=b, symmetric=True)  # b A + c A A
+            gemm_nt_batched(upd, xt, nx, out_t=nxt, d=x, alpha=1.0, beta=a)           # a X + B X
+            x, nx = nx, x
+            xt, nxt = nxt, xt
+    return xt if transposed else x

@@ -58,3 +58,81 @@ def test_newton_schulz_matches_float64_restatement():
         assert rel < 2e-2, (shape, rel)
         s = np.linalg.svd(got.astype(np.float64), compute_uv=False)
         assert s.max() < 1.3 and s.min() > 0.5, s  # quintic NS pushes singular values into ~[0.7, 1.2]
+
+
+def _nt_batched(a, b, out, out_t=None, d=None, alpha=1.0, beta=0.0, symmetric=False):
+    from gefen_amd.newton_schulz import gemm_nt_batched
+
+    gemm_nt_batched(a, b, out, out_t=out_t, d=d, alpha=alpha, beta=beta, symmetric=symmetric)
+
+
+@pytest.mark.parametrize("g,m,n,k,alpha,beta,sym", [
+    (3, 256, 512, 96, 1.0, 0.0, False),
+    (2, 512, 256, 320, 1.7, -0.6, False),
+    (4, 512, 512, 768, 1.0, 0.0, True),
+    (2, 768, 768, 768, 2.0315, -4.775, True),
+])
+def test_batched_gemm_equals_one_matrix_gemm(g, m, n, k, alpha, beta, sym):
+    """The batched large-tile GEMM accumulates K in the same MFMA order as the
+    one-matrix kernel: results are bit-identical, C^T is C transposed, and a
+    symmetric product's mirrored tiles equal the computed ones."""
+    from gefen_amd.newton_schulz import gemm
+
+    gen = torch.Generator(device="cpu").manual_seed(g * 1000 + m + n + k)
+    a = (torch.randn(g, m, k, generator=gen) * 0.05).bfloat16().cuda()
+    if sym:
+        b = a
+        d = (a.float() @ a.float().transpose(1, 2)).bfloat16().contiguous()  # symmetric D
+    else:
+        b = (torch.randn(g, n, k, generator=gen) * 0.05).bfloat16().cuda()
+        d = (torch.randn(g, m, n, generator=gen) * 0.05).bfloat16().cuda()
+    out = torch.empty(g, m, n, dtype=torch.bfloat16, device="cuda:0")
+    out_t = None if sym else torch.empty(g, n, m, dtype=torch.bfloat16, device="cuda:0")
+    _nt_batched(a, b, out, out_t=out_t, d=d if beta != 0.0 else None, alpha=alpha, beta=beta, symmetric=sym)
+    ref = torch.empty_like(out)
+    for i in range(g):
+        gemm(a[i], b[i], True, ref[i], d=d[i] if beta != 0.0 else None, alpha=alpha, beta=beta)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    other = out if sym else out_t  # a symmetric product equals its transpose
+    assert torch.equal(other.view(torch.int16), out.transpose(1, 2).contiguous().view(torch.int16))
+
+
+def test_batched_gemm_rejects_untiled_shapes():
+    from gefen_amd import _lib
+    from gefen_amd.newton_schulz import gemm_nt_batched
+
+    a = torch.zeros(2, 200, 64, dtype=torch.bfloat16, device="cuda:0")
+    out = torch.empty(2, 200, 200, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(ValueError):
+        gemm_nt_batched(a, a, out, symmetric=True)
+    b = torch.zeros(2, 256, 64, dtype=torch.bfloat16, device="cuda:0")
+    out2 = torch.empty(2, 256, 512, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(ValueError):  # symmetric needs a square product
+        gemm_nt_batched(b, torch.zeros(2, 512, 64, dtype=torch.bfloat16, device="cuda:0"), out2, symmetric=True)
+    sq = torch.empty(2, 256, 256, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(ValueError):  # no separate transposed output for a symmetric product
+        gemm_nt_batched(b, b, sq, out_t=torch.empty_like(sq), symmetric=True)
+    assert _lib.GefenError is not None
+
+
+@pytest.mark.parametrize("g,rows,cols", [(3, 256, 512), (2, 512, 256), (2, 256, 256)])
+def test_batched_newton_schulz_matches_one_matrix_path(g, rows, cols):
+    """Stacked Newton-Schulz equals the per-matrix path (same products, same
+    rounding points) and the float64 restatement within the NS tolerance."""
+    from gefen_amd.newton_schulz import newton_schulz_batched, newton_schulz_bf16
+    from oracle import oracle as orc
+
+    gen = torch.Generator(device="cpu").manual_seed(rows * 3 + cols)
+    x = torch.randn(g, rows, cols, generator=gen) * 1e-3
+    got = newton_schulz_batched(x.bfloat16().cuda(), (3.4445, -4.7750, 2.0315), 5, 1e-7)
+    for i in range(g):
+        one = newton_schulz_bf16(x[i].cuda(), (3.4445, -4.7750, 2.0315), 5, 1e-7)
+        # the two paths differ only in how torch reduces the norm; when the bf16
+        # norms agree the results are bit-identical
+        d = (got[i].float() - one.float()).abs().max().item()
+        assert d <= 2.0 ** -6, (i, d)
+        ref = orc.newton_schulz_bf16(x[i].numpy())
+        gi = got[i].float().cpu().numpy()
+        rel = np.linalg.norm(gi - ref) / np.linalg.norm(ref)
+        assert rel < 2e-2, (i, rel)
