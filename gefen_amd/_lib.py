@@ -40,6 +40,8 @@ SIGNATURES = {
     "gefen_automatic_muon_momentum": (I32, [P, I32, P, P, I32, P, I32, P, I32, I64, I64, DBL, P]),
     "gefen_step_tasks": (I32, [P, I32, P, P]),
     "gefen_muon_tasks": (I32, [P, I32, P, P]),
+    "gefen_ns_prepare": (I32, [P, P, I32, I32, I32, DBL, P]),
+    "gefen_muon_apply_tasks": (I32, [P, I32, P]),
     "gefen_exact_histogram": (I32, [P, I32, I64, I64, P, I32, P]),
     "gefen_accumulate_counts": (I32, [P, P, I32, P]),
     "gefen_exact_dp_workspace_size": (SZ, [I32, I32]),
@@ -69,7 +71,11 @@ MUON_TASK = np.dtype([
     ("numel", np.int64), ("block", np.int64), ("grad_dtype", np.int32), ("state_dtype", np.int32),
     ("momentum", np.float64), ("nesterov", np.int32), ("pad", np.int32),
 ])
-assert STEP_TASK.itemsize == 128 and MUON_TASK.itemsize == 72
+MUON_APPLY_TASK = np.dtype([
+    ("p", np.uint64), ("update", np.uint64), ("numel", np.int64), ("param_dtype", np.int32),
+    ("transposed", np.int32), ("lr", np.float64), ("weight_decay", np.float64), ("adjusted_lr", np.float64),
+])
+assert STEP_TASK.itemsize == 128 and MUON_TASK.itemsize == 72 and MUON_APPLY_TASK.itemsize == 56
 
 _LIB = None
 

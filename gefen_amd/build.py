@@ -32,7 +32,7 @@ COMMON = [
 ]
 
 LIBS = {
-    "libgefen_hip.so": ["capi.cpp", "step.hip", "codebook.hip", "period.hip", "ns_gemm.hip"],
+    "libgefen_hip.so": ["capi.cpp", "step.hip", "codebook.hip", "period.hip", "ns_gemm.hip", "muon.hip"],
     "libgefen_synth.so": ["capi.cpp", "synthetic.hip"],
 }
 

@@ -36,5 +36,8 @@ int hip_status(hipError_t e, const char* what) {
 extern "C" const char* gefen_last_error(void) { return g_error; }
 extern "C" int gefen_abi_version(void) { return 1; }
 extern "C" size_t gefen_struct_size(int which) {
-    return which == 0 ? sizeof(gefen_step_task) : which == 1 ? sizeof(gefen_muon_task) : 0;
+    return which == 0   ? sizeof(gefen_step_task)
+           : which == 1 ? sizeof(gefen_muon_task)
+           : which == 2 ? sizeof(gefen_muon_apply_task)
+                        : 0;
 }

@@ -3,8 +3,9 @@
 Muon with Gefen's 8-bit quantised momentum.  Per step, one batched HIP launch
 updates the quantised momentum of every tensor and writes the Nesterov blend
 (gefen_muon.py:302-316, CPU-path rounding); Newton-Schulz orthogonalisation
-(gefen_muon.py:16-51) runs on the device; the parameter update follows the
-reference's CPU arithmetic (gefen_muon.py:325-329).
+(gefen_muon.py:16-51) runs batched over same-shaped matrices on MFMA; the
+parameter update is one batched launch with the reference's CPU arithmetic
+(gefen_muon.py:325-329).
 """
 
 from __future__ import annotations
@@ -60,24 +61,6 @@ def _adjust_lr(lr: float, adjust_lr_fn: Optional[str], param_shape: torch.Size) 
     else:
         ratio = 1.0
     return lr * ratio
-
-
-def _apply_update(p: torch.Tensor, update: torch.Tensor, lr: float, weight_decay: float, adjusted_lr: float,
-                  transposed: bool) -> None:
-    """p.mul_(1 - lr*wd); p.add_(update, alpha=-adjusted_lr) with the reference's
-    CPU rounding (gefen_muon.py:325-329): reduced dtypes round alpha to the
-    dtype, and the element-wise path of a transposed update also rounds the
-    product; fp32 is one fused multiply-add."""
-    if weight_decay > 0.0:
-        p.mul_(1 - lr * weight_decay)
-    if p.dtype == torch.float32:
-        p.add_(update.float(), alpha=-adjusted_lr)
-        return
-    alpha = torch.tensor(-adjusted_lr, dtype=torch.float32).to(p.dtype).float().item()
-    prod = update.float() * alpha
-    if transposed:
-        prod = prod.to(p.dtype).float()
-    p.copy_((p.float() + prod).to(p.dtype))
 
 
 class GefenMuon(Gefen):
@@ -227,13 +210,16 @@ class GefenMuon(Gefen):
                 res = newton_schulz_batched(x, coeffs, steps, eps)
                 for slot, i in enumerate(idx):
                     updates[i] = res[slot]
+        apply = np.zeros(len(items), dtype=_lib.MUON_APPLY_TASK)
+        copy_back = []
         for i, ((group, p, local_p, grad), out) in enumerate(zip(items, outs)):
             st = self.state[p]
             st["step"] += 1
             update = updates.get(i)
             if update is None:
                 update = _zeropower_via_newtonschulz(out.view_as(grad), group["ns_coefficients"], group["ns_steps"],
-                                                     group["eps"])
+                                                     group["eps"]).contiguous()
+            keep.append(update)
             lr = group["lr"]
             lr = float(lr.item()) if torch.is_tensor(lr) else float(lr)
             adjusted = _adjust_lr(lr, group["adjust_lr_fn"], p.shape)
@@ -241,12 +227,25 @@ class GefenMuon(Gefen):
                 target = local_p
             elif hasattr(p, "to_local") and hasattr(p, "placements"):
                 target = local_p.contiguous()
+                copy_back.append((local_p, target))
             else:
                 raise ValueError("GefenMuon fused update requires a contiguous parameter tensor for {}.".format(
                     group["name"]))
-            _apply_update(target, update, lr, group["weight_decay"], adjusted, grad.size(0) > grad.size(1))
-            if target is not local_p:
-                local_p.copy_(target)
+            keep.append(target)
+            t = apply[i]
+            t["p"] = target.data_ptr()
+            t["update"] = update.data_ptr()
+            t["numel"] = target.numel()
+            t["param_dtype"] = _DTYPE_CODE[target.dtype]
+            t["transposed"] = 1 if grad.size(0) > grad.size(1) else 0
+            t["lr"] = lr
+            t["weight_decay"] = group["weight_decay"]
+            t["adjusted_lr"] = adjusted
+        with torch.cuda.device(dev):
+            rc = lib.gefen_muon_apply_tasks(apply.ctypes.data, len(items), torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(rc, "gefen_muon_apply_tasks")
+        for local_p, target in copy_back:
+            local_p.copy_(target)
         del keep
 
     @torch.no_grad()

@@ -91,14 +91,14 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
     a, b, c = coeffs
     g, rows, cols = x.shape
     transposed = rows > cols
-    # normalise each matrix: x /= max(||x||, eps) in bf16 (gefen_muon.py:37)
-    nrm = torch.linalg.vector_norm(x.view(g, -1), dim=1).clamp(min=eps)
-    x.div_(nrm.view(g, 1, 1))
-    # X [G, m, n] with m <= n and its transpose
-    if transposed:
-        xt, x = x, x.transpose(1, 2).contiguous()
-    else:
-        xt = x.transpose(1, 2).contiguous()
+    # normalise each matrix, x /= max(||x||, eps) in bf16 (gefen_muon.py:37), and
+    # write its transpose: X [G, m, n] with m <= n and X^T
+    other = torch.empty(g, cols, rows, dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        _lib.check(lib.gefen_ns_prepare(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps),
+                                        torch.cuda.current_stream(x.device).cuda_stream), "gefen_ns_prepare")
+    x, xt = (other, x) if transposed else (x, other)
     m, n = x.shape[1], x.shape[2]
     gram = torch.empty(g, m, m, dtype=torch.bfloat16, device=x.device)
     upd = torch.empty_like(gram)

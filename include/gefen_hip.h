@@ -34,7 +34,8 @@ enum { GEFEN_F32 = 0, GEFEN_F16 = 1, GEFEN_BF16 = 2 };
 
 const char* gefen_last_error(void);
 int gefen_abi_version(void);
-/* sizeof(gefen_step_task) for which = 0, sizeof(gefen_muon_task) for which = 1:
+/* sizeof(gefen_step_task) for which = 0, sizeof(gefen_muon_task) for which = 1,
+ * sizeof(gefen_muon_apply_task) for which = 2:
  * lets bindings check their mirror of the structs. */
 size_t gefen_struct_size(int which);
 
@@ -138,6 +139,31 @@ typedef struct gefen_muon_task {
 
 int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* tables,
                      gefen_stream_t stream);
+
+/* Replaces the bf16 normalisation before Newton-Schulz (gefen_muon.py:37,
+ * ortho_grad.div_(ortho_grad.norm().clamp(min=eps)), done by torch in the
+ * reference) for a stack of `batch` bf16 matrices [rows, cols] (contiguous):
+ * x[g] = bf16(x[g] / max(bf16(||x[g]||), bf16(eps))) in place, and
+ * xt[g] = x[g]^T [cols, rows].  rows and cols multiples of 64. */
+int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols, double eps, gefen_stream_t stream);
+
+/* Replaces the parameter update of gefen_muon.py:325-329 (p.mul_(1 - lr*wd);
+ * p.add_(update, alpha=-lr_adj)) with the reference's CPU rounding: reduced
+ * dtypes round alpha to the dtype, and round the product first when the
+ * update came back transposed (rows > cols); fp32 is one fused multiply-add.
+ * update: numel bf16 values in the parameter's layout. */
+typedef struct gefen_muon_apply_task {
+    void* p;
+    const void* update;
+    int64_t numel;
+    int32_t param_dtype;
+    int32_t transposed;
+    double lr;
+    double weight_decay;
+    double adjusted_lr;
+} gefen_muon_apply_task;
+
+int gefen_muon_apply_tasks(const gefen_muon_apply_task* tasks, int ntasks, gefen_stream_t stream);
 
 /* ------------------------------------------------------------------ first step
  * Replaces gefen_exact_histogram_cuda (exact_histogram_fused.py:10-58,

@@ -31,6 +31,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
     assert lib.gefen_struct_size(0) == _lib.STEP_TASK.itemsize
     assert lib.gefen_struct_size(1) == _lib.MUON_TASK.itemsize
+    assert lib.gefen_struct_size(2) == _lib.MUON_APPLY_TASK.itemsize
     assert lib.gefen_abi_version() == 1
 
 
