@@ -38,6 +38,7 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "optimizer step ms at GPT-2 125M / Llama-1.5B / 8B shapes; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 
 
 def llama_shapes(hidden, layers, q_out, kv_out, inter, vocab):
@@ -152,6 +153,48 @@ def kernel_tasks(opt, params):
         t["bias_correction_1"] = 1 - g["beta1"] ** (st["step"] + 1)
         t["bias_correction_2"] = 1 - g["beta2"] ** (st["step"] + 1)
     return tasks
+
+
+def muon_ns_roofline(opt, params, reps=3):
+    """Newton-Schulz of one GefenMuon step (the batched stacks the optimizer builds,
+    on bf16 inputs of the same shapes) timed with HIP events on the launch stream.
+    Algorithmic flops per matrix and iteration: 2 (m^2 n + m^3 + m^2 n), m = min
+    dim, n = max dim (X X^T, A A, B X), as the reference computes them."""
+    from gefen_amd.newton_schulz import batched_shape_ok, newton_schulz_batched
+
+    groups = {}
+    for _, p in params:
+        rows, cols = p.shape
+        if batched_shape_ok(rows, cols):
+            groups[(rows, cols)] = groups.get((rows, cols), 0) + 1
+    g0 = opt.param_groups[0]
+    coeffs, steps, eps = tuple(g0["ns_coefficients"]), g0["ns_steps"], g0["eps"]
+    dev = params[0][1].device
+    stacks = {k: (torch.randn(n, k[0], k[1], device=dev) * 1e-3).bfloat16() for k, n in groups.items()}
+    flops = 0.0
+    for (rows, cols), n in groups.items():
+        m, nn = min(rows, cols), max(rows, cols)
+        flops += n * steps * 2.0 * (m * m * nn + m * m * m + m * m * nn)
+    stream = torch.cuda.current_stream()
+
+    def run():  # x is renormalised in place each time: the same work every call
+        for x in stacks.values():
+            newton_schulz_batched(x, coeffs, steps, eps)
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel_ms_per_step": round(ms, 3), "algorithmic_flops_per_step": flops,
+            "note": "Newton-Schulz of every stack of one step, normalisation included"}
 
 
 def cpu_baseline(opt, params, budget_s=20.0):
@@ -283,6 +326,8 @@ def main():
                            "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes)}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline(opt, params)
+    else:
+        out["roofline"] = muon_ns_roofline(opt, params)
     print(json.dumps(out), flush=True)
 
 

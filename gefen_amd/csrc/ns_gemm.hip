@@ -193,14 +193,19 @@ __global__ __launch_bounds__(NT) void k_gemm(const uint16_t* __restrict__ A, int
 // (the Gram matrix X X^T, A A with A symmetric, and B X with X^T kept beside X).
 // A 512-thread workgroup owns a 256x256 tile; its eight waves (2 x 4) each own
 // 128x64 as 4x2 v_mfma_f32_32x32x16_bf16 tiles (128 fp32 accumulators per
-// lane).  K moves
-// 32 at a time: two register stages and two LDS stages give a prefetch distance
-// of two steps.  Symmetric outputs (X X^T, b A + c A A) compute only the tiles
-// on and above the diagonal and mirror them; CT (optional) receives C^T.
-// M and N must be multiples of 256, K a multiple of 32, every row 16-byte
+// lane).  K moves TK (64) at a time: two register stages and two LDS stages
+// give a prefetch distance of two steps.  Symmetric outputs (X X^T, b A + c A A)
+// compute only the tiles on and above the diagonal and mirror them; CT
+// (optional) receives C^T.  Each XCD takes a contiguous run of tiles, in bands
+// of kGroupM tile rows, so workgroups that share operand panels share an L2.
+// M and N must be multiples of 256, K a multiple of TK, every row 16-byte
 // aligned; other shapes take k_gemm.
-constexpr int TM = 256, TN = 256, TK = 32;
-constexpr int TLD = TK + 8;  // LDS row: 40 bf16 = 80 bytes
+#ifndef GEFEN_NS_TK
+#define GEFEN_NS_TK 64
+#endif
+constexpr int TM = 256, TN = 256, TK = GEFEN_NS_TK;
+constexpr int TLD = TK + 8;  // padded LDS row (bf16 elements)
+constexpr int CPR = TK / 8;  // 16-byte chunks per tile row
 constexpr int TT = 512;
 constexpr int WI = 4, WJ = 2;  // 32x32 MFMA tiles per wave (rows, columns)
 constexpr int TCH = TM * TK / 8 / TT;  // 16-byte chunks per thread per operand tile
@@ -220,29 +225,48 @@ struct TileGemm {
     int symmetric;
 };
 
-// The TCH 16-byte chunks of this thread in a 256 x 32 operand tile: chunk q =
-// threadIdx.x + TT i is row q / 4, k-chunk q % 4.
+// The TCH 16-byte chunks of this thread in a 256 x TK operand tile: chunk q =
+// threadIdx.x + TT i is row q / CPR, k-chunk q % CPR.
 __device__ __forceinline__ void tile_load(const uint16_t* __restrict__ src, int64_t ld, int r0, int k0,
                                           u32x4 out[TCH]) {
 #pragma unroll
     for (int i = 0; i < TCH; ++i) {
         const int q = threadIdx.x + TT * i;
-        out[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + (q >> 2)) * ld + k0 + (q & 3) * 8);
+        out[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + q / CPR) * ld + k0 + (q % CPR) * 8);
     }
 }
 __device__ __forceinline__ void tile_store(uint16_t* lds, const u32x4 in[TCH]) {
 #pragma unroll
     for (int i = 0; i < TCH; ++i) {
         const int q = threadIdx.x + TT * i;
-        *reinterpret_cast<u32x4*>(lds + (q >> 2) * TLD + (q & 3) * 8) = in[i];
+        *reinterpret_cast<u32x4*>(lds + (q / CPR) * TLD + (q % CPR) * 8) = in[i];
     }
+}
+
+#ifndef GEFEN_NS_XCD
+#define GEFEN_NS_XCD 1
+#endif
+#ifndef GEFEN_NS_GROUP_M
+#define GEFEN_NS_GROUP_M 8
+#endif
+constexpr int kXcds = 8;                 // workgroups go round-robin to the 8 XCDs
+constexpr int kGroupM = GEFEN_NS_GROUP_M;  // tile rows per band of the tile order
+
+// Logical tile index of this workgroup: consecutive logical tiles run on one
+// XCD (which shares one L2), instead of the hardware's round-robin.
+__device__ __forceinline__ int logical_block(int b, int nwg) {
+    if (!GEFEN_NS_XCD) return b;
+    const int q = nwg / kXcds, r = nwg % kXcds;
+    const int x = b % kXcds, k = b / kXcds;
+    return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
 
 __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * TLD];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][TN * TLD];
-    const int batch = blockIdx.x / g.tiles;
-    int t = blockIdx.x - batch * g.tiles;
+    const int lb = logical_block(blockIdx.x, gridDim.x);
+    const int batch = lb / g.tiles;
+    int t = lb - batch * g.tiles;
     int ti, tj;
     if (g.symmetric) {  // tiles (ti, tj), ti <= tj, row by row
         ti = 0;
@@ -251,9 +275,13 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
             ++ti;
         }
         tj = ti + t;
-    } else {
-        ti = t / g.tiles_n;
-        tj = t - ti * g.tiles_n;
+    } else {  // bands of kGroupM tile rows, column by column within a band
+        const int tiles_m = g.M / TM;
+        const int band = t / (kGroupM * g.tiles_n);
+        const int rows_in = min(kGroupM, tiles_m - band * kGroupM);
+        const int w = t - band * kGroupM * g.tiles_n;
+        ti = band * kGroupM + w % rows_in;
+        tj = w / rows_in;
     }
     const int m0 = ti * TM, n0 = tj * TN;
     const uint16_t* __restrict__ A = g.A + batch * g.sa;
@@ -385,7 +413,7 @@ extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t st
     if (symmetric && m != n) return fail_inval("a symmetric GEMM must be square");
     if (symmetric && ct) return fail_inval("a symmetric GEMM has no separate transposed output (C^T = C)");
     if (m % ns::TM || n % ns::TN || k % ns::TK || k == 0)
-        return fail_inval("batched GEMM needs M, N multiples of 256 and K a multiple of 32 (got %d, %d, %d)", m, n, k);
+        return fail_inval("batched GEMM needs M, N multiples of 256 and K a multiple of %d (got %d, %d, %d)", ns::TK, m, n, k);
     const void* ptrs[5] = {a, b, c, ct, d};
     const int64_t lds_[5] = {lda, ldb, ldc, ldct, ldd};
     const int64_t strides[5] = {stride_a, stride_b, stride_c, stride_ct, stride_d};

@@ -248,7 +248,7 @@ int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int 
  * [n, m].  symmetric = 1 declares C_b symmetric (m == n, e.g. X X^T, or
  * b A + c A A for a symmetric A): only tiles on and above the diagonal are
  * computed and mirrored (ct must then be NULL: C^T = C).  m and n must be
- * multiples of 256, k a multiple of 32,
+ * multiples of 256, k a multiple of 64,
  * rows 16-byte aligned (else ValueError; gefen_gemm_bf16 takes any shape). */
 int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
                                int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, void* ct,

@@ -67,8 +67,8 @@ def _nt_batched(a, b, out, out_t=None, d=None, alpha=1.0, beta=0.0, symmetric=Fa
 
 
 @pytest.mark.parametrize("g,m,n,k,alpha,beta,sym", [
-    (3, 256, 512, 96, 1.0, 0.0, False),
-    (2, 512, 256, 320, 1.7, -0.6, False),
+    (3, 256, 512, 128, 1.0, 0.0, False),
+    (2, 512, 256, 384, 1.7, -0.6, False),
     (4, 512, 512, 768, 1.0, 0.0, True),
     (2, 768, 768, 768, 2.0315, -4.775, True),
 ])
