@@ -131,6 +131,19 @@ def step_bytes(opt, params):
     return total
 
 
+def measured_traffic(cfg, nbytes):
+    """HBM bytes per step of the k_gefen_step launches from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known
+    size), when they were taken on this workload with the same algorithmic bytes."""
+    path = REPO / "profiles" / "k_gefen_step_llama8b_traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text())
+    if rec.get("workload") != cfg["workload"] or rec.get("algorithmic_bytes_per_step") != int(nbytes):
+        return None
+    return rec["traffic_bytes_per_step"]
+
+
 def kernel_tasks(opt, params):
     """The task array the optimizer passes to gefen_step_tasks (for direct timing)."""
     from gefen_amd import _lib
@@ -253,7 +266,7 @@ def main():
     ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="also copy 2 GiB device-to-device once (a known-size kernel for HBM counter scaling)")
+                    help="also copy 2 GiB once with k_copy16 (a kernel of known traffic for scaling HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
@@ -266,9 +279,11 @@ def main():
     from gefen_amd import _lib
 
     if args.copy_probe:
-        src = torch.empty(1 << 30, dtype=torch.int16, device=dev)
+        from gefen_amd import synthetic as syn
+
+        src = torch.ones(1 << 30, dtype=torch.int16, device=dev)
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        syn.copy_device(src, dst)  # k_copy16: 2 GiB read + 2 GiB written
         torch.cuda.synchronize()
         del src, dst
     params = build_problem(cfg, dev)
@@ -322,7 +337,7 @@ def main():
         nbytes = step_bytes(opt, params)
         achieved = nbytes / (kms * 1e-3) / 1e9
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg, nbytes),
                            "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes)}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline(opt, params)

@@ -75,9 +75,30 @@ __global__ void k_fill(T* __restrict__ out, int64_t n, int64_t cols, uint64_t ke
 }
 
 }  // namespace synth
+namespace synth {
+// Plain copy of 16-byte vectors: a kernel of known traffic (n bytes read, n
+// written) for scaling the HBM byte counters of the profiler.
+__global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n16) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
+}  // namespace synth
 }  // namespace gefen
 
 using namespace gefen;
+
+extern "C" int gefen_synth_copy(const void* src, void* dst, int64_t nbytes, gefen_stream_t hstream) {
+    if (nbytes < 0 || nbytes % 16 || (nbytes > 0 && (!src || !dst))) return fail_inval("bad copy size");
+    if (!aligned(src, 16) || !aligned(dst, 16)) return fail_inval("copy buffers must be 16-byte aligned");
+    const int64_t n16 = nbytes / 16;
+    if (n16 == 0) return GEFEN_OK;
+    const int64_t blocks = (n16 + 255) / 256;
+    if (blocks > INT32_MAX) return fail_inval("copy too large");
+    hipLaunchKernelGGL(synth::k_copy16, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(hstream),
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
+    return launch_status("gefen_synth_copy");
+}
 
 extern "C" int gefen_synth_fill(void* out, int dtype, int64_t numel, int64_t cols, uint64_t seed, uint64_t stream,
                                 int e_lo, int e_hi, int kind, double mult, gefen_stream_t hstream) {

@@ -142,6 +142,8 @@ def _synth_lib():
         lib.gefen_synth_fill.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                          ctypes.c_double, ctypes.c_void_p]
+        lib.gefen_synth_copy.restype = ctypes.c_int
+        lib.gefen_synth_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
         lib.gefen_last_error.restype = ctypes.c_char_p
         _SYNTH = lib
     return _SYNTH
@@ -167,5 +169,20 @@ def fill_device(t, seed: int, stream: int, kind: int, cols: int = 0, e_lo: int =
         rc = _synth_lib().gefen_synth_fill(t.data_ptr(), code, n, cols, seed & 0xFFFFFFFFFFFFFFFF,
                                            stream & 0xFFFFFFFFFFFFFFFF, e_lo, e_hi, kind, float(mult),
                                            torch.cuda.current_stream(t.device).cuda_stream)
+    if rc:
+        raise RuntimeError(_synth_lib().gefen_last_error().decode())
+
+
+def copy_device(src, dst) -> None:
+    """dst <- src with a plain 16-byte-vector copy kernel (known traffic: the
+    bytes of src read once and written once), for scaling profiler counters."""
+    import torch
+
+    n = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != n or not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("copy_device needs two contiguous tensors of the same size")
+    with torch.cuda.device(src.device):
+        rc = _synth_lib().gefen_synth_copy(src.data_ptr(), dst.data_ptr(), n,
+                                           torch.cuda.current_stream(src.device).cuda_stream)
     if rc:
         raise RuntimeError(_synth_lib().gefen_last_error().decode())
