@@ -1,6 +1,6 @@
 """Gefen optimizer-step benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama8b|llama1.5b|gpt2|muon]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config llama8b|llama1.5b|gpt2|muon|kernels]
 
 Prints ONE JSON line.  The default workload is BASELINE.json's north star: a
 Llama-3-8B-shaped parameter set (291 tensors, 8.03e9 bf16 parameters, bf16
@@ -89,6 +89,93 @@ CONFIGS = {
                  workload="GefenMuon step on Qwen3-1.7B-shaped 2D matrices (196 tensors, bf16)"),
 }
 PUBLISHED_MS = {"gpt2": 3.0, "llama1.5b": 29.0}  # README.md:142-145 (hardware not stated)
+KERNELS_WORKLOAD = "Isolated kernel workload: one fp32 tensor of 64M elements (8192x8192), 1e-3 * Student-t(3)"
+
+
+def bench_kernels(args, dev):
+    """the first-step kernels on one 64M-element fp32 tensor,
+    each timed with HIP events on the launch stream (median of reps)."""
+    from gefen_amd import synthetic as syn
+    from gefen_amd.gefen import Gefen
+    from gefen_amd.kernels.exact_histogram_fused import gefen_exact_histogram_cuda
+    from gefen_amd.kernels.lloyd_max_fused import gefen_lloyd_accumulate_cuda, gefen_lloyd_mse_cuda
+    from gefen_amd.kernels.period_variance import (average_within_block_variance_cuda_kernel, period_scores_launch,
+                                                   period_scores_workspace_bytes)
+    from gefen_amd.partitioning import PeriodScorer, candidate_divisors
+    from gefen_amd.quantization import exact_dp_from_counts
+
+    n = 8192 * 8192
+    g = torch.empty(n, dtype=torch.float32, device=dev)
+    syn.fill_device(g, 2026, 2, syn.KIND_STUDENT_T3, mult=1e-3)
+    stream = torch.cuda.current_stream()
+    reps = max(args.steps, 3)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        return statistics.median(ms)
+
+    divs = candidate_divisors(n)
+    ws = torch.empty(period_scores_workspace_bytes(n, divs), dtype=torch.uint8, device=dev)
+    sc = torch.empty(len(divs) + 1, dtype=torch.float64, device=dev)
+    scorer = PeriodScorer(mode=1)
+    scorer.add(g)
+    period = scorer.finish()[0]
+    hist_period = period
+    counts = torch.zeros(4096, dtype=torch.int64, device=dev)
+    gefen_exact_histogram_cuda(g, hist_period, counts)
+    cb = exact_dp_from_counts(counts.float(), 256, True)
+    sums = torch.zeros(256, dtype=torch.float32, device=dev)
+    lc = torch.zeros(256, dtype=torch.int64, device=dev)
+    m1 = torch.zeros(1, dtype=torch.float32, device=dev)
+    m2 = torch.zeros(1, dtype=torch.float32, device=dev)
+    vper = period if period > 1 else 256
+    nbytes = 4.0 * n
+    res = {}
+    res["period_scores"] = timed(lambda: period_scores_launch(g, divs, 1, 1e-12, sc, ws))
+    res["histogram"] = timed(lambda: gefen_exact_histogram_cuda(g, hist_period, counts))
+    res["exact_dp"] = timed(lambda: exact_dp_from_counts(counts.float(), 256, True))
+    res["lloyd_accumulate"] = timed(lambda: gefen_lloyd_accumulate_cuda(g, cb, hist_period, sums, lc))
+    res["lloyd_mse"] = timed(lambda: gefen_lloyd_mse_cuda(g, cb, cb, hist_period, m1, m2))
+    res["block_variance"] = timed(lambda: average_within_block_variance_cuda_kernel(g, vper, input_is_squared=False))
+
+    p = torch.empty(8192, 8192, dtype=torch.float32, device=dev)
+    syn.fill_device(p, 2026, 3, syn.KIND_NORMAL, mult=0.02)
+    p.requires_grad_(True)
+    p.grad = g.view(8192, 8192)
+
+    def first_step():
+        opt = Gefen([("w", p)])
+        opt.step()
+
+    res["gefen_first_step"] = timed(first_step)
+    kernels = {}
+    for k, ms in res.items():
+        kernels[k] = {"ms": round(ms, 4)}
+        if k in ("period_scores", "histogram", "lloyd_accumulate", "lloyd_mse", "block_variance"):
+            kernels[k]["read_GB_s"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    pipeline = res["period_scores"] + res["histogram"] + res["exact_dp"]
+    ach = nbytes / (res["period_scores"] * 1e-3) / 1e9
+    out = {"metric": METRIC, "value": round(pipeline, 4), "unit": "ms", "n_gpus": 1, "steps": reps,
+           "warmup": 1, "ms_per_step": round(pipeline, 4), "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": KERNELS_WORKLOAD, "value_is": "period scores (all {} divisors) + histogram + "
+                      "exact DP, the codebook pipeline of a first step".format(len(divs)),
+                      "period": period, "divisors": len(divs)},
+           "kernels": kernels,
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": "period scores: one read of the 256 MB tensor for all divisors"}}
+    print(json.dumps(out), flush=True)
+
 
 
 def build_problem(cfg, dev, seed=2026):
@@ -263,7 +350,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS) + ["kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 2 GiB once with k_copy16 (a kernel of known traffic for scaling HBM counters)")
@@ -272,8 +359,11 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
               "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
+    if args.config == "kernels":
+        bench_kernels(args, dev)
+        return
+    cfg = CONFIGS[args.config]
     from gefen_amd.gefen import Gefen
     from gefen_amd.gefen_muon import GefenMuon
     from gefen_amd import _lib
