@@ -55,7 +55,7 @@ SIGNATURES = {
     "gefen_lloyd_mse": (I32, [P, I32, I64, I64, P, P, I32, P, P, P]),
     "gefen_gemm_bf16": (I32, [P, I64, P, I64, I32, P, I64, P, I64, I32, I32, I32, DBL, DBL, P]),
     "gefen_gemm_bf16_nt_batched": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, I32,
-                                         I32, I32, DBL, DBL, I32, P]),
+                                         I32, I32, I32, DBL, DBL, I32, P]),
 }
 
 # numpy mirror of struct gefen_step_task / gefen_muon_task (natural C alignment)

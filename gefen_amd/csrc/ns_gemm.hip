@@ -223,6 +223,7 @@ struct TileGemm {
     int tiles_n;   // N / TN
     int tiles;     // tiles per matrix
     int symmetric;
+    int d_t;       // D is given as D^T [N, M] (row stride ldd): four rows of one column are one 8-byte load
 };
 
 // The TCH 16-byte chunks of this thread in a 256 x TK operand tile: chunk q =
@@ -260,6 +261,11 @@ __device__ __forceinline__ int logical_block(int b, int nwg) {
     const int x = b % kXcds, k = b / kXcds;
     return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
+
+// Workgroup barrier for LDS traffic only: this wave's LDS reads and writes are
+// complete, global loads may still be in flight (__syncthreads would also wait
+// for them, which would cut the prefetch short).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * TLD];
@@ -308,36 +314,52 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     tile_store(Bs[0], rb0);
     __syncthreads();
     // one K step from LDS stage CUR; register stage CUR refills with step kt + 2
+    // (clamped to the last step, so the loads are unconditional and the wait
+    // before the LDS stores leaves exactly those loads in flight).  Fragments
+    // of the next 16-deep slice are read while the current slice's MFMAs run.
+#define GEFEN_LOAD_FRAGS(AS, BS, KK, AF, BF)                                                                      \
+    {                                                                                                             \
+        _Pragma("unroll") for (int i = 0; i < WI; ++i) AF[i] =                                                    \
+            *reinterpret_cast<const bf16x8*>((AS) + (wm + i * 32 + (lane & 31)) * TLD + (KK) + 8 * (lane >> 5));  \
+        _Pragma("unroll") for (int j = 0; j < WJ; ++j) BF[j] =                                                    \
+            *reinterpret_cast<const bf16x8*>((BS) + (wn + j * 32 + (lane & 31)) * TLD + (KK) + 8 * (lane >> 5));  \
+    }
+#define GEFEN_MFMAS(AF, BF)                                                                                       \
+    _Pragma("unroll") for (int i = 0; i < WI; ++i) _Pragma("unroll") for (int j = 0; j < WJ; ++j) acc[i][j] =     \
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(AF[i], BF[j], acc[i][j], 0, 0, 0);
 #define GEFEN_TILE_STEP(KT, CUR, RA, RB, RA_NEXT, RB_NEXT)                                                       \
     {                                                                                                             \
-        if ((KT) + 2 < nk) { /* register stage CUR was stored to LDS already */                                   \
-            tile_load(A, g.lda, m0, ((KT) + 2) * TK, RA);                                                         \
-            tile_load(B, g.ldb, n0, ((KT) + 2) * TK, RB);                                                         \
-        }                                                                                                         \
+        const int kpre = min((KT) + 2, nk - 1) * TK;                                                              \
+        tile_load(A, g.lda, m0, kpre, RA);                                                                        \
+        tile_load(B, g.ldb, n0, kpre, RB);                                                                        \
         const uint16_t* as = As[CUR];                                                                             \
         const uint16_t* bs = Bs[CUR];                                                                             \
-        _Pragma("unroll") for (int kk = 0; kk < TK; kk += 16) {                                                   \
-            bf16x8 af[WI], bfr[WJ];                                                                               \
-            _Pragma("unroll") for (int i = 0; i < WI; ++i) af[i] =                                                \
-                *reinterpret_cast<const bf16x8*>(as + (wm + i * 32 + (lane & 31)) * TLD + kk + 8 * (lane >> 5));  \
-            _Pragma("unroll") for (int j = 0; j < WJ; ++j) bfr[j] =                                               \
-                *reinterpret_cast<const bf16x8*>(bs + (wn + j * 32 + (lane & 31)) * TLD + kk + 8 * (lane >> 5));  \
-            _Pragma("unroll") for (int i = 0; i < WI; ++i) _Pragma("unroll") for (int j = 0; j < WJ; ++j)          \
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);           \
+        bf16x8 af0[WI], bf0[WJ], af1[WI], bf1[WJ];                                                                \
+        GEFEN_LOAD_FRAGS(as, bs, 0, af0, bf0)                                                                     \
+        _Pragma("unroll") for (int kk = 0; kk < TK; kk += 32) {                                                   \
+            GEFEN_LOAD_FRAGS(as, bs, kk + 16, af1, bf1)                                                           \
+            GEFEN_MFMAS(af0, bf0)                                                                                 \
+            if (kk + 32 < TK) GEFEN_LOAD_FRAGS(as, bs, kk + 32, af0, bf0)                                         \
+            GEFEN_MFMAS(af1, bf1)                                                                                 \
         }                                                                                                         \
         if ((KT) + 1 < nk) {                                                                                      \
             tile_store(As[(CUR) ^ 1], RA_NEXT);                                                                   \
             tile_store(Bs[(CUR) ^ 1], RB_NEXT);                                                                   \
         }                                                                                                         \
-        __syncthreads();                                                                                          \
+        lds_barrier();                                                                                            \
     }
-    for (int kt = 0; kt < nk; kt += 2) {
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
         GEFEN_TILE_STEP(kt, 0, ra0, rb0, ra1, rb1)
-        if (kt + 1 < nk) GEFEN_TILE_STEP(kt + 1, 1, ra1, rb1, ra0, rb0)
+        GEFEN_TILE_STEP(kt + 1, 1, ra1, rb1, ra0, rb0)
     }
+    if (kt < nk) GEFEN_TILE_STEP(kt, 0, ra0, rb0, ra1, rb1)
 #undef GEFEN_TILE_STEP
+#undef GEFEN_MFMAS
+#undef GEFEN_LOAD_FRAGS
     // epilogue: C = alpha * acc + beta * D rounded once; four consecutive rows of
-    // one column go to CT (and to the mirror tile) as one 8-byte store
+    // one column go to CT (and to the mirror tile) as one 8-byte store, and come
+    // from D^T as one 8-byte load
     uint16_t* __restrict__ C = g.C + batch * g.sc;
     uint16_t* __restrict__ CT = g.CT ? g.CT + batch * g.sct : nullptr;
     const uint16_t* __restrict__ D = g.D ? g.D + batch * g.sd : nullptr;
@@ -345,22 +367,38 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
 #pragma unroll
     for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < WJ; ++j)
+        for (int j = 0; j < WJ; ++j) {
+            const int col = n0 + wn + j * 32 + (lane & 31);
+            float dv[4][4];
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const int col = n0 + wn + j * 32 + (lane & 31);
+                const int row0 = m0 + wm + i * 32 + 8 * r4 + 4 * (lane >> 5);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dv[r4][r] = 0.0f;
+                if (D) {
+                    if (g.d_t) {
+                        const uint2 w = *reinterpret_cast<const uint2*>(D + (int64_t)col * g.ldd + row0);
+                        dv[r4][0] = __uint_as_float(w.x << 16);
+                        dv[r4][1] = __uint_as_float(w.x & 0xffff0000u);
+                        dv[r4][2] = __uint_as_float(w.y << 16);
+                        dv[r4][3] = __uint_as_float(w.y & 0xffff0000u);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            dv[r4][r] = __uint_as_float((uint32_t)D[(int64_t)(row0 + r) * g.ldd + col] << 16);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
                 const int row0 = m0 + wm + i * 32 + 8 * r4 + 4 * (lane >> 5);
                 uint16_t o[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int row = row0 + r;
                     float v = g.alpha * acc[i][j][4 * r4 + r];
-                    if (D) {
-                        const float d = __uint_as_float((uint32_t)D[(int64_t)row * g.ldd + col] << 16);
-                        v = v + g.beta * d;
-                    }
+                    if (D) v = v + g.beta * dv[r4][r];
                     o[r] = from_f32<bf16_t>(v).bits;
-                    C[(int64_t)row * g.ldc + col] = o[r];
+                    C[(int64_t)(row0 + r) * g.ldc + col] = o[r];
                 }
                 uint2 packed;
                 packed.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
@@ -368,6 +406,7 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
                 if (CT) *reinterpret_cast<uint2*>(CT + (int64_t)col * g.ldct + row0) = packed;
                 if (mirror) *reinterpret_cast<uint2*>(C + (int64_t)col * g.ldc + row0) = packed;
             }
+        }
 }
 
 }  // namespace ns
@@ -403,12 +442,12 @@ extern "C" int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_
 extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
                                           int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, void* ct,
                                           int64_t ldct, int64_t stride_ct, const void* d, int64_t ldd,
-                                          int64_t stride_d, int batch, int m, int n, int k, double alpha,
-                                          double beta, int symmetric, gefen_stream_t stream) {
+                                          int64_t stride_d, int d_transposed, int batch, int m, int n, int k,
+                                          double alpha, double beta, int symmetric, gefen_stream_t stream) {
     if (m < 0 || n < 0 || k < 0 || batch < 0) return fail_inval("negative GEMM size");
     if (m == 0 || n == 0 || batch == 0) return GEFEN_OK;
     if (!a || !b || !c || (beta != 0.0 && !d)) return fail_inval("null GEMM operand");
-    if (lda < k || ldb < k || ldc < n || (ct && ldct < m) || (d && ldd < n))
+    if (lda < k || ldb < k || ldc < n || (ct && ldct < m) || (d && ldd < (d_transposed ? m : n)))
         return fail_inval("GEMM leading dimension too small");
     if (symmetric && m != n) return fail_inval("a symmetric GEMM must be square");
     if (symmetric && ct) return fail_inval("a symmetric GEMM has no separate transposed output (C^T = C)");
@@ -436,6 +475,8 @@ extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t st
     g.tiles_n = n / ns::TN;
     g.symmetric = symmetric ? 1 : 0;
     g.tiles = symmetric ? g.tiles_n * (g.tiles_n + 1) / 2 : (m / ns::TM) * g.tiles_n;
+    g.d_t = d_transposed ? 1 : 0;
+    if (g.D && d_transposed && ldd % 4) return fail_inval("D^T rows must be 8-byte aligned");
     const int64_t grid = (int64_t)g.tiles * batch;
     if (grid > INT32_MAX) return fail_inval("batched GEMM grid too large");
     hipLaunchKernelGGL(ns::k_gemm_tile, dim3((unsigned)grid), dim3(ns::TT), 0, reinterpret_cast<hipStream_t>(stream), g);

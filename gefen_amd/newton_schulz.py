@@ -62,8 +62,15 @@ def batched_shape_ok(rows: int, cols: int) -> bool:
 
 
 def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: torch.Tensor = None,
-                    d: torch.Tensor = None, alpha: float = 1.0, beta: float = 0.0, symmetric: bool = False) -> None:
-    """out[i] = alpha * a[i] @ b[i]^T + beta * d[i] (and out_t[i] = out[i]^T) for stacked bf16 matrices."""
+                    d: torch.Tensor = None, alpha: float = 1.0, beta: float = 0.0, symmetric: bool = False,
+                    d_t: torch.Tensor = None) -> None:
+    """out[i] = alpha * a[i] @ b[i]^T + beta * D[i] (and out_t[i] = out[i]^T) for stacked bf16
+    matrices; D is given as d, or as its transpose d_t (read four rows at a time)."""
+    if d is not None and d_t is not None:
+        raise ValueError("give D as d or as d_t, not both")
+    transposed_d = d_t is not None
+    if transposed_d:
+        d = d_t
     g, m, k = a.shape
     n = b.shape[1]
     lib = _lib.load()
@@ -79,8 +86,9 @@ def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: 
 
     rc = lib.gefen_gemm_bf16_nt_batched(a.data_ptr(), a.stride(1), a.stride(0), b.data_ptr(), b.stride(1), b.stride(0),
                                         out.data_ptr(), out.stride(1), out.stride(0), ptr(out_t), ld(out_t), bs(out_t),
-                                        ptr(d), ld(d), bs(d), g, m, n, k, float(alpha), float(beta),
-                                        1 if symmetric else 0, torch.cuda.current_stream(a.device).cuda_stream)
+                                        ptr(d), ld(d), bs(d), 1 if transposed_d else 0, g, m, n, k, float(alpha),
+                                        float(beta), 1 if symmetric else 0,
+                                        torch.cuda.current_stream(a.device).cuda_stream)
     _lib.check(rc, "gefen_gemm_bf16_nt_batched")
 
 
@@ -106,8 +114,8 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
     with torch.cuda.device(x.device):
         for _ in range(steps):
             gemm_nt_batched(x, x, gram, symmetric=True)                                # X X^T
-            gemm_nt_batched(gram, gram, upd, d=gram, alpha=c, beta=b, symmetric=True)  # b A + c A A
-            gemm_nt_batched(upd, xt, nx, out_t=nxt, d=x, alpha=1.0, beta=a)           # a X + B X
+            gemm_nt_batched(gram, gram, upd, d_t=gram, alpha=c, beta=b, symmetric=True)  # b A + c A A
+            gemm_nt_batched(upd, xt, nx, out_t=nxt, d_t=xt, alpha=1.0, beta=a)           # a X + B X
             x, nx = nx, x
             xt, nxt = nxt, xt
     return xt if transposed else x

@@ -245,7 +245,10 @@ int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int 
  *   C_b = alpha * A_b @ B_b^T + beta * D_b,  A_b [m, k], B_b [n, k], C_b, D_b [m, n]
  * row-major bf16 with matrix strides stride_* (elements); fp32 accumulation on
  * MFMA, one rounding to bf16.  ct (optional, may be NULL) receives C_b^T
- * [n, m].  symmetric = 1 declares C_b symmetric (m == n, e.g. X X^T, or
+ * [n, m].  d_transposed = 1: d holds D_b^T [n, m] (row stride ldd), which the
+ * kernel reads four rows at a time (the Gram matrix is its own transpose, and
+ * Newton-Schulz keeps X^T beside X).  symmetric = 1 declares C_b symmetric
+ * (m == n, e.g. X X^T, or
  * b A + c A A for a symmetric A): only tiles on and above the diagonal are
  * computed and mirrored (ct must then be NULL: C^T = C).  m and n must be
  * multiples of 256, k a multiple of 64,
@@ -253,8 +256,8 @@ int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int 
 int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
                                int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, void* ct,
                                int64_t ldct, int64_t stride_ct, const void* d, int64_t ldd, int64_t stride_d,
-                               int batch, int m, int n, int k, double alpha, double beta, int symmetric,
-                               gefen_stream_t stream);
+                               int d_transposed, int batch, int m, int n, int k, double alpha, double beta,
+                               int symmetric, gefen_stream_t stream);
 
 #ifdef __cplusplus
 }

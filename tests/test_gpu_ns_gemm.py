@@ -60,19 +60,21 @@ def test_newton_schulz_matches_float64_restatement():
         assert s.max() < 1.3 and s.min() > 0.5, s  # quintic NS pushes singular values into ~[0.7, 1.2]
 
 
-def _nt_batched(a, b, out, out_t=None, d=None, alpha=1.0, beta=0.0, symmetric=False):
+def _nt_batched(a, b, out, out_t=None, d=None, alpha=1.0, beta=0.0, symmetric=False, d_t=None):
     from gefen_amd.newton_schulz import gemm_nt_batched
 
-    gemm_nt_batched(a, b, out, out_t=out_t, d=d, alpha=alpha, beta=beta, symmetric=symmetric)
+    gemm_nt_batched(a, b, out, out_t=out_t, d=d, alpha=alpha, beta=beta, symmetric=symmetric, d_t=d_t)
 
 
-@pytest.mark.parametrize("g,m,n,k,alpha,beta,sym", [
-    (3, 256, 512, 128, 1.0, 0.0, False),
-    (2, 512, 256, 384, 1.7, -0.6, False),
-    (4, 512, 512, 768, 1.0, 0.0, True),
-    (2, 768, 768, 768, 2.0315, -4.775, True),
+@pytest.mark.parametrize("g,m,n,k,alpha,beta,sym,dt", [
+    (3, 256, 512, 128, 1.0, 0.0, False, False),
+    (2, 512, 256, 384, 1.7, -0.6, False, False),
+    (2, 512, 768, 256, 1.0, 3.4445, False, True),
+    (4, 512, 512, 768, 1.0, 0.0, True, False),
+    (2, 768, 768, 768, 2.0315, -4.775, True, False),
+    (2, 512, 512, 512, 2.0315, -4.775, True, True),
 ])
-def test_batched_gemm_equals_one_matrix_gemm(g, m, n, k, alpha, beta, sym):
+def test_batched_gemm_equals_one_matrix_gemm(g, m, n, k, alpha, beta, sym, dt):
     """The batched large-tile GEMM accumulates K in the same MFMA order as the
     one-matrix kernel: results are bit-identical, C^T is C transposed, and a
     symmetric product's mirrored tiles equal the computed ones."""
@@ -88,7 +90,11 @@ def test_batched_gemm_equals_one_matrix_gemm(g, m, n, k, alpha, beta, sym):
         d = (torch.randn(g, m, n, generator=gen) * 0.05).bfloat16().cuda()
     out = torch.empty(g, m, n, dtype=torch.bfloat16, device="cuda:0")
     out_t = None if sym else torch.empty(g, n, m, dtype=torch.bfloat16, device="cuda:0")
-    _nt_batched(a, b, out, out_t=out_t, d=d if beta != 0.0 else None, alpha=alpha, beta=beta, symmetric=sym)
+    if dt and beta != 0.0:  # D passed as its transpose
+        _nt_batched(a, b, out, out_t=out_t, d_t=d.transpose(1, 2).contiguous(), alpha=alpha, beta=beta,
+                    symmetric=sym)
+    else:
+        _nt_batched(a, b, out, out_t=out_t, d=d if beta != 0.0 else None, alpha=alpha, beta=beta, symmetric=sym)
     ref = torch.empty_like(out)
     for i in range(g):
         gemm(a[i], b[i], True, ref[i], d=d[i] if beta != 0.0 else None, alpha=alpha, beta=beta)
