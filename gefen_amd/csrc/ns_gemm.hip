@@ -206,8 +206,12 @@ __global__ __launch_bounds__(NT) void k_gemm(const uint16_t* __restrict__ A, int
 constexpr int TM = 256, TN = 256, TK = GEFEN_NS_TK;
 constexpr int TLD = TK + 8;  // padded LDS row (bf16 elements)
 constexpr int CPR = TK / 8;  // 16-byte chunks per tile row
-constexpr int TT = 512;
-constexpr int WI = 4, WJ = 2;  // 32x32 MFMA tiles per wave (rows, columns)
+#ifndef GEFEN_NS_WJ
+#define GEFEN_NS_WJ 2
+#endif
+constexpr int WI = 4, WJ = GEFEN_NS_WJ;  // 32x32 MFMA tiles per wave (rows, columns)
+constexpr int WAVES_N = TN / (32 * WJ), WAVES_M = TM / (32 * WI);
+constexpr int TT = 64 * WAVES_M * WAVES_N;
 constexpr int TCH = TM * TK / 8 / TT;  // 16-byte chunks per thread per operand tile
 
 struct TileGemm {
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     const uint16_t* __restrict__ A = g.A + batch * g.sa;
     const uint16_t* __restrict__ B = g.B + batch * g.sb;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 2) * (32 * WI), wn = (wave & 3) * (32 * WJ);
+    const int wm = (wave / WAVES_N) * (32 * WI), wn = (wave % WAVES_N) * (32 * WJ);
     f32x16 acc[WI][WJ];
 #pragma unroll
     for (int i = 0; i < WI; ++i)
