@@ -1,0 +1,66 @@
+"""Tensors past 2^31 elements.  Every output of the step depends only on its own
+magnitude block, the codebook and scalars, so the last blocks of a tensor of
+more than 2^31 elements, stepped inside it, must equal the same blocks stepped
+as a tensor of their own -- bit for bit, through two steps."""
+
+import numpy as np
+import pytest
+import torch
+
+import gpu_util as gu
+from golden_util import load
+from gefen_amd import _lib
+from gefen_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+
+def _tables():
+    data, _ = load("exact_dp")
+    cb = torch.from_numpy(np.ascontiguousarray(data["hist_k256_forced/codebook"], dtype=np.float32)).to("cuda:0")
+    lib = _lib.load()
+    t = torch.empty(int(lib.gefen_codebook_tables_size()), dtype=torch.uint8, device="cuda:0")
+    _lib.check(lib.gefen_prepare_codebook(cb.data_ptr(), cb.numel(), t.data_ptr(), gu.stream()))
+    return t
+
+
+@pytest.mark.parametrize("period", [2048, 1])
+def test_blocks_past_2_31_elements_match_a_tensor_of_their_own(period):
+    print("large tensor, period", period, flush=True)
+    n = 2048 * (2 ** 20 + 64)  # 2^31 + 131072 elements
+    tail = 2048 * 64
+    assert n > 2 ** 31
+    dev = "cuda:0"
+    pod = 256 if period == 1 else 0
+    blk = pod if period == 1 else period
+    p = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    g = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    syn.fill_device(p, 31, 1, syn.KIND_NORMAL, mult=0.02)
+    syn.fill_device(g, 31, 2, syn.KIND_ROW_SCALED, cols=2048, e_lo=-17, e_hi=-7)
+    idx = torch.zeros(n, dtype=torch.uint8, device=dev)
+    mag = torch.zeros(n // blk, dtype=torch.bfloat16, device=dev)
+    vm = torch.zeros(n // period, dtype=torch.bfloat16, device=dev)
+    # the last `tail` elements as a tensor of their own
+    ps, gs = p[-tail:].clone(), g[-tail:].clone()
+    idxs = torch.zeros(tail, dtype=torch.uint8, device=dev)
+    mags = torch.zeros(tail // blk, dtype=torch.bfloat16, device=dev)
+    vms = torch.zeros(tail // period, dtype=torch.bfloat16, device=dev)
+    tables = _tables()
+    lib = _lib.load()
+    tasks = np.zeros(2, dtype=_lib.STEP_TASK)
+    for t, (pp, gg, ii, mm, vv, nn) in zip(tasks, [(p, g, idx, mag, vm, n), (ps, gs, idxs, mags, vms, tail)]):
+        t["p"], t["grad"], t["m_codebook"] = pp.data_ptr(), gg.data_ptr(), ii.data_ptr()
+        t["m_magnitude"], t["vmean"] = mm.data_ptr(), vv.data_ptr()
+        t["numel"], t["period"], t["period_one_divisor"] = nn, period, pod
+        t["param_dtype"] = t["state_dtype"] = gu.CODE["bf16"]
+        t["beta1"], t["beta2"], t["lr"], t["eps"], t["weight_decay"] = 0.9, 0.999, 1e-3, 1e-8, 0.01
+    for step in (1, 2):
+        tasks["bias_correction_1"] = 1 - 0.9 ** step
+        tasks["bias_correction_2"] = 1 - 0.999 ** step
+        _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, 2, tables.data_ptr(), gu.stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(p[-tail:].view(torch.int16), ps.view(torch.int16))
+    assert torch.equal(idx[-tail:], idxs)
+    assert torch.equal(mag[-(tail // blk):].view(torch.int16), mags.view(torch.int16))
+    assert torch.equal(vm[-(tail // period):].view(torch.int16), vms.view(torch.int16))
+    assert int(idxs.to(torch.int32).sum()) > 0  # the step did quantise something
