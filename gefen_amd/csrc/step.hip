@@ -16,6 +16,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "capi_internal.h"
@@ -620,6 +621,173 @@ __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
 }
 
 // ---------------------------------------------------------------------------
+// Packed 4-bit codebook indices (automatic_gefen_fused_kernel.cu:14-57): the
+// index of element e is the low nibble of byte e/2 when e is even and the high
+// nibble when e is odd, and a stored index keeps its low four bits only.  A lane
+// owns whole bytes, so both nibbles of a byte inside one row go out in one plain
+// byte store.  A byte shared by two rows (odd period), or holding the last
+// element of an odd-length tensor, is changed by one atomic xor of old ^ new on
+// the row's own nibble: xors of disjoint nibbles commute, so both rows' nibbles
+// land and the nibble past the tensor's end keeps its bits.  No other lane
+// writes a lane's own nibble, so the byte it loaded holds that nibble's old value.
+//
+// G lanes per row (16, 64 or 256), kThreads / G rows per workgroup; the
+// workgroups stride over the rows.
+constexpr int kPackedMaxGrid = 65536;
+
+__device__ __forceinline__ void store_nibbles(uint8_t* idx, int64_t b, uint32_t oldb, int k0, int k1, bool in0,
+                                              bool in1) {
+    if (in0 && in1) {
+        idx[b] = (uint8_t)((k0 & 15) | ((k1 & 15) << 4));
+        return;
+    }
+    const uint32_t x = in0 ? (((uint32_t)k0 ^ oldb) & 15u) : ((((uint32_t)k1 ^ (oldb >> 4)) & 15u) << 4);
+    if (x == 0) return;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(idx + b);
+    atomicXor(reinterpret_cast<unsigned int*>(a & ~(uintptr_t)3), x << (8u * (uint32_t)(a & 3)));
+}
+
+// Max over the G lanes of a row; for G = 256 through LDS, with a barrier on each
+// side so every lane has read the row's old magnitude and red[] is free again.
+template <int G>
+__device__ __forceinline__ float packed_row_max(float mx, float* red) {
+    if constexpr (G <= 64) {
+        return group_max(mx, G);
+    } else {
+        mx = group_max(mx, 64);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        const float r = nanmax(nanmax(red[0], red[1]), nanmax(red[2], red[3]));
+        __syncthreads();
+        return r;
+    }
+}
+
+// Gefen update with a given stepsize or given vmean (rows of `rowlen`), packed indices.
+template <typename D, typename S, int G>
+__global__ __launch_bounds__(kThreads) void k_gefen_step_packed(const StepBatch B) {
+    __shared__ LdsTables L;
+    __shared__ float red[4];
+    int K;
+    load_tables<D, kThreads>(L, B.tables, K);
+    const StepTask& T = B.t[0];
+    constexpr bool QROUND = sizeof(D) == sizeof(S);
+    constexpr int RPW = kThreads / G;
+    const int sub = threadIdx.x / G, t = threadIdx.x % G;
+    D* __restrict__ p = static_cast<D*>(T.p);
+    const D* __restrict__ g = static_cast<const D*>(T.g);
+    uint8_t* idx = T.idx;
+    S* __restrict__ mag = static_cast<S*>(T.mag);
+    const S* __restrict__ vm = static_cast<const S*>(T.vmean);
+    for (int64_t r0 = (int64_t)blockIdx.x * RPW; r0 < T.nrows; r0 += (int64_t)gridDim.x * RPW) {
+        const int64_t row = r0 + sub;
+        const bool active = row < T.nrows;
+        const int64_t e_lo = row * T.rowlen, e_hi = e_lo + T.rowlen;
+        const int64_t b_lo = e_lo >> 1, b_hi = (e_hi + 1) >> 1;
+        const float mold = active ? to_f32(mag[row]) : 0.0f;
+        auto momentum = [&](int64_t e, uint32_t old) -> float {
+            const float gf = to_f32(g[e]);
+            const float cur = L.cbd[old] * mold;
+            return __builtin_fmaf(T.b1c, gf - cur, cur);
+        };
+        float mx = 0.0f;
+        if (active) {
+            for (int64_t b = b_lo + t; b < b_hi; b += G) {
+                const uint32_t ob = idx[b];
+                const int64_t e0 = 2 * b;
+                if (e0 >= e_lo) mx = nanmax(mx, fabsf(momentum(e0, ob & 15u)));
+                if (e0 + 1 < e_hi) mx = nanmax(mx, fabsf(momentum(e0 + 1, ob >> 4)));
+            }
+        }
+        mx = packed_row_max<G>(mx, red);
+        if (!active) continue;
+        const S mag_s = from_f32<S>(mx);
+        const float mn = to_f32(mag_s);
+        const float ss = T.mode == kVmeanGiven ? stepsize_of(to_f32(vm[row]), T) : T.stepsize[row];
+        if (t == 0) mag[row] = mag_s;
+        auto update = [&](int64_t e, uint32_t old) -> int {
+            const float u = momentum(e, old);
+            const float x = (mn > 0.0f) ? u / mn : 0.0f;
+            const int k = nearest_fast(x, L.thr, L.bucket, K);
+            float q = L.cbd[k] * mn;
+            if (QROUND) q = round_to<D>(q);
+            const float uu = (q * ss) * T.lr;
+            float pf = to_f32(p[e]);
+            if (T.do_wd) pf = round_to<D>(pf * T.wdf);
+            p[e] = from_f32<D>(pf - uu);
+            return k;
+        };
+        for (int64_t b = b_lo + t; b < b_hi; b += G) {
+            const uint32_t ob = idx[b];
+            const int64_t e0 = 2 * b;
+            const bool in0 = e0 >= e_lo, in1 = e0 + 1 < e_hi;
+            const int k0 = in0 ? update(e0, ob & 15u) : 0;
+            const int k1 = in1 ? update(e0 + 1, ob >> 4) : 0;
+            store_nibbles(idx, b, ob, k0, k1, in0, in1);
+        }
+    }
+}
+
+// GefenMuon quantised momentum (as k_muon_long), packed indices.
+template <typename D, typename S, int G>
+__global__ __launch_bounds__(kThreads) void k_muon_packed(const MuonBatch B) {
+    __shared__ LdsTables L;
+    __shared__ float red[4];
+    int K;
+    load_tables<D, kThreads>(L, B.tables, K);
+    const MuonTask& T = B.t[0];
+    constexpr int RPW = kThreads / G;
+    const int sub = threadIdx.x / G, t = threadIdx.x % G;
+    const D* __restrict__ g = static_cast<const D*>(T.g);
+    uint8_t* idx = T.idx;
+    S* __restrict__ mag = static_cast<S*>(T.mag);
+    D* __restrict__ out = static_cast<D*>(T.out);
+    for (int64_t r0 = (int64_t)blockIdx.x * RPW; r0 < T.nrows; r0 += (int64_t)gridDim.x * RPW) {
+        const int64_t row = r0 + sub;
+        const bool active = row < T.nrows;
+        const int64_t e_lo = row * T.rowlen, e_hi = e_lo + T.rowlen;
+        const int64_t b_lo = e_lo >> 1, b_hi = (e_hi + 1) >> 1;
+        const float mold = active ? to_f32(mag[row]) : 0.0f;
+        auto lerped = [&](int64_t e, uint32_t old) -> float {
+            const float gf = to_f32(g[e]);
+            const float m0 = round_to<D>(L.cbd[old] * mold);
+            return round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));
+        };
+        float mx = 0.0f;
+        if (active) {
+            for (int64_t b = b_lo + t; b < b_hi; b += G) {
+                const uint32_t ob = idx[b];
+                const int64_t e0 = 2 * b;
+                if (e0 >= e_lo) mx = nanmax(mx, fabsf(lerped(e0, ob & 15u)));
+                if (e0 + 1 < e_hi) mx = nanmax(mx, fabsf(lerped(e0 + 1, ob >> 4)));
+            }
+        }
+        mx = packed_row_max<G>(mx, red);
+        if (!active) continue;
+        const S mag_s = from_f32<S>(mx);
+        const float ms = to_f32(mag_s);
+        const float clamped = (ms < T.tiny) ? T.tiny : ms;
+        if (t == 0) mag[row] = mag_s;
+        auto requant = [&](int64_t e, uint32_t old) -> int {
+            float x = round_to<D>(lerped(e, old) / clamped);
+            if (ms <= 0.0f) x = 0.0f;
+            const int k = nearest_fast(x, L.thr, L.bucket, K);
+            const float q = round_to<D>(L.cbd[k] * ms);
+            out[e] = from_f32<D>(muon_out<D, S>(q, to_f32(g[e]), T));
+            return k;
+        };
+        for (int64_t b = b_lo + t; b < b_hi; b += G) {
+            const uint32_t ob = idx[b];
+            const int64_t e0 = 2 * b;
+            const bool in0 = e0 >= e_lo, in1 = e0 + 1 < e_hi;
+            const int k0 = in0 ? requant(e0, ob & 15u) : 0;
+            const int k1 = in1 ? requant(e0 + 1, ob >> 4) : 0;
+            store_nibbles(idx, b, ob, k0, k1, in0, in1);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Stepsize table of a period-one tensor with a 16-bit state: lut[b] is the
 // stepsize (gefen.py:1326-1327) of the non-negative state value with bits b,
 // computed by the same expression as the per-block path, so lookups are exact.
@@ -772,6 +940,44 @@ hipError_t dispatch_muon(const Key& k, const MuonBatch& b, int grid, hipStream_t
     if (k.d == GEFEN_F16 && k.s == GEFEN_F16) return launch_muon<f16_t, f16_t>(k, b, grid, st);
     if (k.d == GEFEN_BF16 && k.s == GEFEN_F32) return launch_muon<bf16_t, float>(k, b, grid, st);
     if (k.d == GEFEN_F16 && k.s == GEFEN_F32) return launch_muon<f16_t, float>(k, b, grid, st);
+    return hipErrorInvalidValue;
+}
+
+// Packed-index kernels: lanes per row from the row's byte count, grid-stride over rows.
+int packed_lanes(int64_t rowlen) {
+    const int64_t bytes = rowlen / 2 + 1;
+    return bytes <= 32 ? 16 : (bytes <= 512 ? 64 : 256);
+}
+
+int packed_grid(int64_t nrows, int lanes) {
+    const int64_t rpw = kThreads / lanes;
+    return (int)std::min<int64_t>((nrows + rpw - 1) / rpw, kPackedMaxGrid);
+}
+
+template <typename D, typename S, typename BatchT>
+hipError_t launch_packed(const BatchT& b, int64_t rowlen, int64_t nrows, hipStream_t st) {
+    const int G = packed_lanes(rowlen);
+    const int grid = packed_grid(nrows, G);
+#define GEFEN_PACKED_CASE(GG)                                                                                      \
+    if (G == GG) {                                                                                                 \
+        if constexpr (std::is_same<BatchT, MuonBatch>::value)                                                      \
+            hipLaunchKernelGGL((k_muon_packed<D, S, GG>), dim3(grid), dim3(kThreads), 0, st, b);                    \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_gefen_step_packed<D, S, GG>), dim3(grid), dim3(kThreads), 0, st, b);              \
+        return hipGetLastError();                                                                                  \
+    }
+    GEFEN_PACKED_CASE(16) GEFEN_PACKED_CASE(64) GEFEN_PACKED_CASE(256)
+#undef GEFEN_PACKED_CASE
+    return hipErrorInvalidValue;
+}
+
+template <typename BatchT>
+hipError_t dispatch_packed(int d, int s, const BatchT& b, int64_t rowlen, int64_t nrows, hipStream_t st) {
+    if (d == GEFEN_F32) return launch_packed<float, float>(b, rowlen, nrows, st);
+    if (d == GEFEN_BF16 && s == GEFEN_BF16) return launch_packed<bf16_t, bf16_t>(b, rowlen, nrows, st);
+    if (d == GEFEN_F16 && s == GEFEN_F16) return launch_packed<f16_t, f16_t>(b, rowlen, nrows, st);
+    if (d == GEFEN_BF16 && s == GEFEN_F32) return launch_packed<bf16_t, float>(b, rowlen, nrows, st);
+    if (d == GEFEN_F16 && s == GEFEN_F32) return launch_packed<f16_t, float>(b, rowlen, nrows, st);
     return hipErrorInvalidValue;
 }
 
@@ -980,7 +1186,6 @@ static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_
                          const float* codebook, int K, int packed, int64_t num_blocks, int64_t period,
                          int64_t pod, int mode, double beta1, double beta2, double lr, double bc1,
                          double bc2, double eps, gefen_stream_t stream) {
-    if (packed) return fail_inval("packed 4-bit codebook indices are not supported");
     int rc = check_codebook(codebook, K);
     if (rc) return rc;
     if (!valid_dtype(param_dtype)) return fail_inval("unsupported parameter dtype %d", param_dtype);
@@ -1018,6 +1223,15 @@ static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_
     TempTables tt;
     rc = tt.init(codebook, K, st);
     if (rc) return rc;
+    if (packed) {
+        StepBatch b;
+        memset(&b, 0, sizeof(b));
+        b.t[0] = ps.task;
+        b.ntasks = 1;
+        b.tables = static_cast<const CodebookTables*>(tt.ptr);
+        hipError_t e = dispatch_packed(param_dtype, mag_dtype, b, ps.task.rowlen, ps.task.nrows, st);
+        return e == hipSuccess ? GEFEN_OK : hip_status(e, "gefen packed step launch");
+    }
     std::vector<PendingStep> pend(1, ps);
     void* luts = nullptr;
     rc = prepare_luts(pend, st, &luts);
@@ -1171,7 +1385,6 @@ extern "C" int gefen_automatic_muon_momentum(const void* grad, int grad_dtype, u
                                              int codebook_size, void* momentum_update, int packed_indices,
                                              int64_t num_blocks, int64_t period, double beta1,
                                              gefen_stream_t stream) {
-    if (packed_indices) return fail_inval("packed 4-bit codebook indices are not supported");
     int rc = check_codebook(codebook, codebook_size);
     if (rc) return rc;
     if (num_blocks < 0 || period <= 0) return fail_inval("Expected a positive period, got %lld", (long long)period);
@@ -1195,6 +1408,15 @@ extern "C" int gefen_automatic_muon_momentum(const void* grad, int grad_dtype, u
     TempTables tt;
     rc = tt.init(codebook, codebook_size, st);
     if (rc) return rc;
+    if (packed_indices) {
+        MuonBatch b;
+        memset(&b, 0, sizeof(b));
+        b.t[0] = pm.task;
+        b.ntasks = 1;
+        b.tables = static_cast<const CodebookTables*>(tt.ptr);
+        hipError_t e = dispatch_packed(grad_dtype, magnitude_dtype, b, pm.task.rowlen, pm.task.nrows, st);
+        return e == hipSuccess ? GEFEN_OK : hip_status(e, "gefen packed muon launch");
+    }
     std::vector<PendingMuon> pend(1, pm);
     return flush_muon(pend, static_cast<const CodebookTables*>(tt.ptr), st);
 }

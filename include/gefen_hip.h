@@ -56,6 +56,13 @@ int gefen_automatic_vmean_update(void* vmean, int vmean_dtype, const void* grad,
                                  gefen_stream_t stream);
 
 /* ------------------------------------------------------------------ fused updates
+ * packed_indices != 0 (here and in gefen_automatic_muon_momentum) selects the
+ * packed 4-bit layout of automatic_gefen_fused_kernel.cu:14-57: m_sign holds
+ * (numel + 1) / 2 bytes; element i's index is the low nibble of byte i/2 for even
+ * i and the high nibble for odd i; a stored index keeps its low four bits (a
+ * codebook of at most 16 entries is the meaningful use) and the other nibble of
+ * its byte is left as it was.
+ *
  * Replaces automatic_gefen_fused_update_cuda (automatic_gefen_fused.py:10-117,
  * automatic_gefen_fused_kernel.cu:568-674): stepsize given per block (f32). */
 int gefen_automatic_fused_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,

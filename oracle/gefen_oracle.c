@@ -11,6 +11,7 @@
  *   stepsize             gefen.py:1326-1327
  *   weight decay         gefen.py:1280-1281
  *   momentum / quantise  gefen.py:1153-1206 (+ nearest 122-143, dequant 146-169)
+ *   packed 4-bit indices automatic_gefen_fused_kernel.cu:14-57 (layout only)
  *   parameter update     gefen.py:1328-1333
  *   histogram            gefen.py:350-366
  *   exact DP codebook    quantization.py:68-81, 151-258 (+ gefen.py:373-399)
@@ -165,7 +166,85 @@ int orc_vmean_update(int sdt, void* vmean, int gdt, const void* g,
 }
 
 /* ------------------------------------------------------------------ update
- * One Gefen step of one tensor on the reference CPU path, after the caller has
+ * Momentum, quantisation and parameter update of one magnitude block of `mblk`
+ * elements starting at s0 (gefen.py:1153-1206, 1328-1333).  The stepsize of
+ * element i is stepsize[i / period] when `stepsize` is non-null, else the
+ * stepsize of vmean[i / period] (gefen.py:1326-1327). */
+typedef struct {
+    int ddt, sdt, qdt, vdt, K, do_wd;
+    void* p;
+    const void* g;
+    uint8_t* idx;
+    void* mag;
+    const void* vmean;
+    const float* stepsize;
+    const float* cb;
+    float cbd[256];
+    int64_t period;
+    float b1c, sqrt_bc2, eps_f, inv_bc1, lr_f, wd_f;
+} StepCtx;
+
+static void step_ctx_init(StepCtx* c, int ddt, int sdt, const float* cb, int K, double beta1, double lr,
+                          double eps, double wd, double bc1, double bc2) {
+    c->ddt = ddt;
+    c->sdt = sdt;
+    /* promote(D, S) of codebook[idx].to(D) * magnitude (gefen.py:1205-1206) */
+    c->qdt = (ddt == sdt) ? ddt : DT_F32;
+    c->cb = cb;
+    c->K = K;
+    /* codebook rounded to the parameter dtype (dequant, gefen.py:160-162, 1205) */
+    for (int k = 0; k < K; ++k) c->cbd[k] = round_dt(cb[k], ddt);
+    c->b1c = (float)(1.0 - beta1);
+    c->sqrt_bc2 = (float)sqrt(bc2);
+    c->eps_f = (float)eps;
+    c->inv_bc1 = (float)(1.0 / bc1);
+    c->lr_f = (float)lr;
+    c->do_wd = wd > 0.0;
+    c->wd_f = (float)(1.0 - lr * wd);
+}
+
+static void quantise_block(const StepCtx* c, int64_t b, int64_t s0, int64_t mblk) {
+    const float mold = load_dt(c->mag, c->sdt, b);
+    float mx = 0.0f;
+    for (int64_t j = 0; j < mblk; ++j) {
+        const int64_t i = s0 + j;
+        float cur = c->cbd[c->idx[i]] * mold;
+        float gf = load_dt(c->g, c->ddt, i);
+        float upd = fmaf(c->b1c, gf - cur, cur);
+        mx = nanmax(mx, fabsf(upd));
+    }
+    store_dt(c->mag, c->sdt, b, mx);
+    const float mn = load_dt(c->mag, c->sdt, b);
+    float ss_row = 0.0f;
+    int64_t cur_vrow = -1;
+    for (int64_t j = 0; j < mblk; ++j) {
+        const int64_t i = s0 + j;
+        float cur = c->cbd[c->idx[i]] * mold;
+        float gf = load_dt(c->g, c->ddt, i);
+        float upd = fmaf(c->b1c, gf - cur, cur);
+        float x = (mn > 0.0f) ? upd / mn : 0.0f;
+        int k = nearest_index(c->cb, c->K, x);
+        c->idx[i] = (uint8_t)k;
+        const int64_t vr = i / c->period;
+        if (vr != cur_vrow) {
+            if (c->stepsize) {
+                ss_row = c->stepsize[vr];
+            } else {
+                float v = load_dt(c->vmean, c->vdt, vr);
+                float h = sqrtf(v) / c->sqrt_bc2 + c->eps_f;
+                ss_row = (1.0f / h) * c->inv_bc1;
+            }
+            cur_vrow = vr;
+        }
+        float q = round_dt(c->cbd[k] * mn, c->qdt);
+        float u = (q * ss_row) * c->lr_f;
+        float pv = load_dt(c->p, c->ddt, i);
+        if (c->do_wd) pv = round_dt(pv * c->wd_f, c->ddt);
+        store_dt(c->p, c->ddt, i, pv - u);
+    }
+}
+
+/* One Gefen step of one tensor on the reference CPU path, after the caller has
  * advanced state["step"] and computed bc1 = 1 - beta1**step, bc2 = 1 - beta2**step
  * in double precision (gefen.py:1278-1284).
  *
@@ -182,19 +261,17 @@ int orc_gefen_step(int ddt, int sdt, void* p, const void* g, uint8_t* idx,
     const int64_t mblk = (period == 1) ? pod : period;
     if (mblk <= 0 || n % mblk != 0) return 1;
     const int64_t mrows = n / mblk;
-    const float b1c = (float)(1.0 - beta1);
     const float b2 = (float)beta2, omb2 = (float)(1.0 - beta2);
-    const float sqrt_bc2 = (float)sqrt(bc2);
-    const float eps_f = (float)eps;
-    const float inv_bc1 = (float)(1.0 / bc1);
-    const float lr_f = (float)lr;
-    const int do_wd = wd > 0.0;
-    const float wd_f = (float)(1.0 - lr * wd);
-    /* codebook rounded to the parameter dtype (dequant, gefen.py:160-162, 1205) */
-    float cbd[256];
-    for (int k = 0; k < K; ++k) cbd[k] = round_dt(cb[k], ddt);
-    /* promote(D, S) of codebook[idx].to(D) * magnitude (gefen.py:1205-1206) */
-    const int qdt = (ddt == sdt) ? ddt : DT_F32;
+    StepCtx c;
+    step_ctx_init(&c, ddt, sdt, cb, K, beta1, lr, eps, wd, bc1, bc2);
+    c.p = p;
+    c.g = g;
+    c.idx = idx;
+    c.mag = mag;
+    c.vmean = vmean;
+    c.vdt = sdt;
+    c.stepsize = NULL;
+    c.period = period;
 
 #ifdef _OPENMP
     if (nthreads <= 0) nthreads = omp_get_max_threads();
@@ -212,42 +289,49 @@ int orc_gefen_step(int ddt, int sdt, void* p, const void* g, uint8_t* idx,
 
     /* 2) momentum, quantisation and parameter update per magnitude block */
 #pragma omp parallel for schedule(static) num_threads(nthreads) if (mrows > 16)
-    for (int64_t b = 0; b < mrows; ++b) {
-        const int64_t s0 = b * mblk;
-        const float mold = load_dt(mag, sdt, b);
-        float mx = 0.0f;
-        for (int64_t j = 0; j < mblk; ++j) {
-            const int64_t i = s0 + j;
-            float cur = cbd[idx[i]] * mold;
-            float gf = load_dt(g, ddt, i);
-            float upd = fmaf(b1c, gf - cur, cur);
-            mx = nanmax(mx, fabsf(upd));
-        }
-        store_dt(mag, sdt, b, mx);
-        const float mn = load_dt(mag, sdt, b);
-        float ss_row = 0.0f;
-        int64_t cur_vrow = -1;
-        for (int64_t j = 0; j < mblk; ++j) {
-            const int64_t i = s0 + j;
-            float cur = cbd[idx[i]] * mold;
-            float gf = load_dt(g, ddt, i);
-            float upd = fmaf(b1c, gf - cur, cur);
-            float x = (mn > 0.0f) ? upd / mn : 0.0f;
-            int k = nearest_index(cb, K, x);
-            idx[i] = (uint8_t)k;
-            const int64_t vr = i / period;
-            if (vr != cur_vrow) {
-                float v = load_dt(vmean, sdt, vr);
-                float h = sqrtf(v) / sqrt_bc2 + eps_f;
-                ss_row = (1.0f / h) * inv_bc1;
-                cur_vrow = vr;
-            }
-            float q = round_dt(cbd[k] * mn, qdt);
-            float u = (q * ss_row) * lr_f;
-            float pv = load_dt(p, ddt, i);
-            if (do_wd) pv = round_dt(pv * wd_f, ddt);
-            store_dt(p, ddt, i, pv - u);
-        }
+    for (int64_t b = 0; b < mrows; ++b) quantise_block(&c, b, b * mblk, mblk);
+    return 0;
+}
+
+/* The update of the reference's given-stepsize and given-vmean entry points
+ * (automatic_gefen_fused.py:10-249) with the CPU-path arithmetic: rows of
+ * `period` elements share m_magnitude and a stepsize, which is stepsize[r] when
+ * `stepsize` is non-null, else the stepsize (gefen.py:1326-1327) of vmean[r]
+ * as given (not updated here).  No weight decay. */
+int orc_gefen_update_given(int ddt, int sdt, void* p, const void* g, uint8_t* idx, void* mag,
+                           const void* vmean, int vdt, const float* stepsize, int64_t n,
+                           int64_t period, const float* cb, int K, double beta1, double lr,
+                           double bc1, double bc2, double eps) {
+    if (n <= 0) return 0;
+    if (period <= 0 || n % period != 0) return 1;
+    StepCtx c;
+    step_ctx_init(&c, ddt, sdt, cb, K, beta1, lr, eps, 0.0, bc1, bc2);
+    c.p = p;
+    c.g = g;
+    c.idx = idx;
+    c.mag = mag;
+    c.vmean = vmean;
+    c.vdt = vdt;
+    c.stepsize = stepsize;
+    c.period = period;
+    for (int64_t b = 0; b < n / period; ++b) quantise_block(&c, b, b * period, period);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ packed indices
+ * The packed 4-bit layout of automatic_gefen_fused_kernel.cu:14-57: the index of
+ * element i is the low nibble of byte i/2 when i is even and the high nibble when
+ * i is odd; storing keeps an index's low four bits and leaves the other nibble of
+ * its byte alone (so the high nibble of the last byte of an odd n is kept). */
+int orc_unpack_nibbles(const uint8_t* packed, int64_t n, uint8_t* idx) {
+    for (int64_t i = 0; i < n; ++i) idx[i] = (i & 1) ? (uint8_t)(packed[i >> 1] >> 4) : (uint8_t)(packed[i >> 1] & 15);
+    return 0;
+}
+
+int orc_pack_nibbles(const uint8_t* idx, int64_t n, uint8_t* packed) {
+    for (int64_t i = 0; i < n; ++i) {
+        const int sh = (i & 1) ? 4 : 0;
+        packed[i >> 1] = (uint8_t)((packed[i >> 1] & ~(15 << sh)) | ((idx[i] & 15) << sh));
     }
     return 0;
 }

@@ -57,9 +57,13 @@ def lib():
         L.orc_f32_to_bf16.argtypes = [P, P, I64]
         L.orc_f32_to_f16.argtypes = [P, P, I64]
         L.orc_fma32.argtypes = [P, ctypes.c_float, P, P, I64]
+        L.orc_gefen_update_given.argtypes = [I, I, P, P, P, P, P, I, P, I64, I64, P, I, D, D, D, D, D]
+        L.orc_unpack_nibbles.argtypes = [P, I64, P]
+        L.orc_pack_nibbles.argtypes = [P, I64, P]
         for name in ("orc_gefen_step", "orc_vmean_update", "orc_nearest", "orc_histogram",
                      "orc_accumulate_counts", "orc_exact_dp", "orc_period_scores",
-                     "orc_muon_momentum", "orc_f32_to_bf16", "orc_f32_to_f16", "orc_fma32"):
+                     "orc_muon_momentum", "orc_f32_to_bf16", "orc_f32_to_f16", "orc_fma32",
+                     "orc_gefen_update_given", "orc_unpack_nibbles", "orc_pack_nibbles"):
             getattr(L, name).restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -335,6 +339,39 @@ def muon_momentum(g: np.ndarray, dtype: str, st: TensorState, codebook: np.ndarr
     if rc:
         raise RuntimeError("orc_muon_momentum failed: {}".format(rc))
     return out
+
+
+def gefen_update_given(dtype: str, sdtype: str, p: np.ndarray, g: np.ndarray, idx: np.ndarray,
+                       mag: np.ndarray, period: int, codebook: np.ndarray, beta1: float, lr: float,
+                       vmean: Optional[np.ndarray] = None, vdtype: Optional[str] = None,
+                       stepsize: Optional[np.ndarray] = None, bc1: float = 1.0, bc2: float = 1.0,
+                       eps: float = 0.0) -> None:
+    """The given-stepsize / given-vmean update (automatic_gefen_fused.py:10-249) on the
+    CPU-path arithmetic; p, idx and mag are updated in place."""
+    gg = np.ascontiguousarray(g.reshape(-1))
+    cb = np.ascontiguousarray(codebook, dtype=np.float32)
+    st = None if stepsize is None else np.ascontiguousarray(stepsize, dtype=np.float32)
+    vm = None if vmean is None else np.ascontiguousarray(vmean)
+    rc = lib().orc_gefen_update_given(
+        DT[dtype], DT[sdtype], _ptr(p), _ptr(gg), _ptr(idx), _ptr(mag), None if vm is None else _ptr(vm),
+        DT[vdtype or sdtype], None if st is None else _ptr(st), gg.size, period, _ptr(cb), cb.size,
+        beta1, lr, bc1, bc2, eps)
+    if rc:
+        raise RuntimeError("orc_gefen_update_given failed: {}".format(rc))
+
+
+def unpack_nibbles(packed: np.ndarray, n: int) -> np.ndarray:
+    """Packed 4-bit indices -> one byte per element (automatic_gefen_fused_kernel.cu:14-27)."""
+    out = np.empty(n, dtype=np.uint8)
+    lib().orc_unpack_nibbles(_ptr(np.ascontiguousarray(packed)), n, _ptr(out))
+    return out
+
+
+def pack_nibbles(idx: np.ndarray, packed: np.ndarray) -> None:
+    """Store idx & 0xF into the nibbles of `packed` in place (automatic_gefen_fused_kernel.cu:29-57)."""
+    idx = np.ascontiguousarray(idx, dtype=np.uint8)
+    assert packed.size == (idx.size + 1) // 2
+    lib().orc_pack_nibbles(_ptr(idx), idx.size, _ptr(packed))
 
 
 class GefenMuonOracle(GefenOracle):

@@ -45,8 +45,8 @@ def test_entry_points_reject_invalid_arguments_without_a_device():
         _lib.check(lib.gefen_exact_histogram(1, 0, 16, 4, 1, 5000, None))
     with pytest.raises(ValueError, match="divisible"):
         _lib.check(lib.gefen_exact_histogram(1, 0, 17, 4, 1, 4096, None))
-    with pytest.raises(ValueError, match="packed"):
-        _lib.check(lib.gefen_automatic_fused_update_from_vmean(1, 1, 0, 1, 1, 0, 1, 0, 1, 256, 1, 4, 4, 0.9, 1e-3,
+    with pytest.raises(ValueError, match="vmean dtype"):
+        _lib.check(lib.gefen_automatic_fused_update_from_vmean(1, 1, 0, 1, 1, 0, 1, 1, 1, 256, 1, 4, 4, 0.9, 1e-3,
                                                                0.5, 0.5, 1e-8, None))
     with pytest.raises(ValueError, match="beta2"):
         _lib.check(lib.gefen_automatic_vmean_update(1, 0, 1, 0, 4, 4, 1.5, None))

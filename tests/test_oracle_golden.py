@@ -137,3 +137,65 @@ def test_gefen_muon_trajectory_matches_reference(name):
                 tol = 0.05 if dt != "f32" else 0.01
                 rel = np.linalg.norm(ours - ref) / max(np.linalg.norm(ref), 1e-30)
                 assert rel <= tol, "{} p{} step {}: relative update error {:.3g}".format(name, i, step, rel)
+
+
+# ------------------------------------------------------------------ kernel-level entry points
+def test_packed_nibble_layout():
+    """automatic_gefen_fused_kernel.cu:14-57: element i's index is the low nibble of byte
+    i/2 for even i and the high nibble for odd i; a store keeps the low four bits of the
+    index and leaves the other nibble of its byte as it was."""
+    packed = np.array([0xFF, 0xAB], np.uint8)
+    orc.pack_nibbles(np.array([1, 2, 19], np.uint8), packed)
+    assert packed.tolist() == [0x21, 0xA3]
+    assert orc.unpack_nibbles(packed, 3).tolist() == [1, 2, 3]
+    assert orc.unpack_nibbles(np.array([0x5A, 0x0F], np.uint8), 4).tolist() == [0xA, 0x5, 0xF, 0x0]
+    rng = np.random.default_rng(3)
+    for n in (1, 2, 7, 64, 1001):
+        idx = rng.integers(0, 256, n, dtype=np.uint8)
+        packed = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+        tail = packed[-1] >> 4
+        orc.pack_nibbles(idx, packed)
+        np.testing.assert_array_equal(orc.unpack_nibbles(packed, n), idx & 15)
+        if n % 2:
+            assert packed[-1] >> 4 == tail
+
+
+@pytest.mark.parametrize("dt,sdt,period", [("f32", "f32", 96), ("bf16", "bf16", 33), ("bf16", "f32", 7),
+                                           ("f16", "f16", 256)])
+def test_given_vmean_and_given_stepsize_updates_equal_the_step(dt, sdt, period):
+    """The given-vmean update after the vmean EMA, and the given-stepsize update with the
+    stepsize of gefen.py:1326-1327 computed here in numpy float32, both equal one step of
+    the (trajectory-pinned) oracle step, bit for bit, through three steps."""
+    from gefen_amd import synthetic as syn
+
+    data, _ = load("exact_dp")
+    cb = np.ascontiguousarray(data["hist_k256_forced/codebook"], dtype=np.float32)
+    rows = 6
+    n = rows * period
+    b1, b2, lr, eps = 0.9, 0.999, 1e-3, 1e-8
+    p0 = syn.round_to(syn.normal(syn.make_key(2, 1), n) * 0.02, dt)
+    st = {k: orc.TensorState(n, period, dt, sdt) for k in "abc"}
+    p = {k: p0.copy() for k in "abc"}
+    vb = st["b"].vmean
+    for step in (1, 2, 3):
+        g = syn.round_to(syn.row_scaled_normal(4, step, rows, period, -14, -4), dt).reshape(-1)
+        bc1, bc2 = 1 - b1 ** step, 1 - b2 ** step
+        a = st["a"]
+        rc = orc.lib().orc_gefen_step(orc.DT[dt], orc.DT[sdt], orc._ptr(p["a"]), orc._ptr(g),
+                                      orc._ptr(a.m_codebook), orc._ptr(a.m_magnitude), orc._ptr(a.vmean), n,
+                                      period, 0, orc._ptr(cb), cb.size, b1, b2, lr, eps, 0.0, bc1, bc2, 1)
+        assert rc == 0
+        orc.lib().orc_vmean_update(orc.DT[sdt], orc._ptr(vb), orc.DT[dt], orc._ptr(g), rows, period, b2)
+        orc.gefen_update_given(dt, sdt, p["b"], g, st["b"].m_codebook, st["b"].m_magnitude, period, cb, b1, lr,
+                               vmean=vb, bc1=bc1, bc2=bc2, eps=eps)
+        v = orc.to_f32(vb, sdt)
+        h = np.sqrt(v) / np.float32(np.sqrt(bc2)) + np.float32(eps)
+        ss = ((np.float32(1.0) / h) * np.float32(1.0 / bc1)).astype(np.float32)
+        orc.gefen_update_given(dt, sdt, p["c"], g, st["c"].m_codebook, st["c"].m_magnitude, period, cb, b1, lr,
+                               stepsize=ss)
+        np.testing.assert_array_equal(vb, a.vmean)
+        for o in "bc":
+            np.testing.assert_array_equal(st[o].m_codebook, a.m_codebook)
+            np.testing.assert_array_equal(st[o].m_magnitude, a.m_magnitude)
+            np.testing.assert_array_equal(p[o], p["a"])
+        assert int(a.m_codebook.astype(np.int64).sum()) > 0
