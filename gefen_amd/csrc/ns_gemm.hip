@@ -271,9 +271,19 @@ __device__ __forceinline__ int logical_block(int b, int nwg) {
 // for them, which would cut the prefetch short).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Epilogue tile in LDS: T[c][r] = C[r][c] (the C^T orientation) in rows of LDT
+// bf16.  LDT / 2 = 130 dwords = 2 (mod 32): the 8-byte accesses of 16
+// consecutive columns cover all 32 banks once, and gathering one row from
+// two column chunks 8 apart (1040 dwords = 16 mod 32) is conflict-free too.
+constexpr int LDT = TM + 4;
+static_assert(TM == TN, "square tiles");
+static_assert(TN * LDT <= 4 * TM * TLD, "the epilogue tile fits in the operand stages");
+
 __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * TLD];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][TN * TLD];
+    // operand stages: A in [0, 2) and B in [2, 4) of TM x TLD each; the epilogue reuses them
+    __shared__ __attribute__((aligned(16))) uint16_t smem[4 * TM * TLD];
+    uint16_t* const As[2] = {smem, smem + TM * TLD};
+    uint16_t* const Bs[2] = {smem + 2 * TM * TLD, smem + 3 * TM * TLD};
     const int lb = logical_block(blockIdx.x, gridDim.x);
     const int batch = lb / g.tiles;
     int t = lb - batch * g.tiles;
@@ -361,56 +371,100 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
 #undef GEFEN_TILE_STEP
 #undef GEFEN_MFMAS
 #undef GEFEN_LOAD_FRAGS
-    // epilogue: C = alpha * acc + beta * D rounded once; four consecutive rows of
-    // one column go to CT (and to the mirror tile) as one 8-byte store, and come
-    // from D^T as one 8-byte load
+    // epilogue: C = alpha * acc + beta * D rounded once, assembled in LDS as
+    // T = C^T (every wave is past its last fragment read: the last K step ended
+    // with a barrier), then written with 16-byte stores: T's rows are rows of
+    // C^T (CT, or the mirror tile of a symmetric product), and C's rows are
+    // gathered from two column chunks per wave instruction.  D given as D^T is
+    // staged through T the same way; a row-major D is read directly.
     uint16_t* __restrict__ C = g.C + batch * g.sc;
     uint16_t* __restrict__ CT = g.CT ? g.CT + batch * g.sct : nullptr;
     const uint16_t* __restrict__ D = g.D ? g.D + batch * g.sd : nullptr;
     const bool mirror = g.symmetric && ti != tj;
+    uint16_t* const T = smem;
+    constexpr int kChunks = TM * TN / 8 / TT;  // 16-byte chunks per thread
+    const bool d_lds = D && g.d_t;
+    if (d_lds) {
+        u32x4 dv[kChunks];
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int q = threadIdx.x + TT * i;
+            const int c = q >> 5, r8 = (q & 31) * 8;
+            dv[i] = *reinterpret_cast<const u32x4*>(D + (int64_t)(n0 + c) * g.ldd + m0 + r8);
+        }
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int q = threadIdx.x + TT * i;
+            const int c = q >> 5, r8 = (q & 31) * 8;
+            uint2* t = reinterpret_cast<uint2*>(T + c * LDT + r8);
+            t[0] = make_uint2(dv[i].x, dv[i].y);
+            t[1] = make_uint2(dv[i].z, dv[i].w);
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int i = 0; i < WI; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
-            const int col = n0 + wn + j * 32 + (lane & 31);
-            float dv[4][4];
+            const int c = wn + j * 32 + (lane & 31);
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const int row0 = m0 + wm + i * 32 + 8 * r4 + 4 * (lane >> 5);
+                const int r0 = wm + i * 32 + 8 * r4 + 4 * (lane >> 5);
+                uint2* t = reinterpret_cast<uint2*>(T + c * LDT + r0);
+                float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (d_lds) {
+                    const uint2 w = *t;
+                    dv[0] = __uint_as_float(w.x << 16);
+                    dv[1] = __uint_as_float(w.x & 0xffff0000u);
+                    dv[2] = __uint_as_float(w.y << 16);
+                    dv[3] = __uint_as_float(w.y & 0xffff0000u);
+                } else if (D) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dv[r4][r] = 0.0f;
-                if (D) {
-                    if (g.d_t) {
-                        const uint2 w = *reinterpret_cast<const uint2*>(D + (int64_t)col * g.ldd + row0);
-                        dv[r4][0] = __uint_as_float(w.x << 16);
-                        dv[r4][1] = __uint_as_float(w.x & 0xffff0000u);
-                        dv[r4][2] = __uint_as_float(w.y << 16);
-                        dv[r4][3] = __uint_as_float(w.y & 0xffff0000u);
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            dv[r4][r] = __uint_as_float((uint32_t)D[(int64_t)(row0 + r) * g.ldd + col] << 16);
-                    }
+                    for (int r = 0; r < 4; ++r)
+                        dv[r] = __uint_as_float((uint32_t)D[(int64_t)(m0 + r0 + r) * g.ldd + n0 + c] << 16);
                 }
-            }
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int row0 = m0 + wm + i * 32 + 8 * r4 + 4 * (lane >> 5);
-                uint16_t o[4];
+                uint32_t o[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     float v = g.alpha * acc[i][j][4 * r4 + r];
-                    if (D) v = v + g.beta * dv[r4][r];
+                    if (D) v = v + g.beta * dv[r];
                     o[r] = from_f32<bf16_t>(v).bits;
-                    C[(int64_t)(row0 + r) * g.ldc + col] = o[r];
                 }
-                uint2 packed;
-                packed.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-                packed.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-                if (CT) *reinterpret_cast<uint2*>(CT + (int64_t)col * g.ldct + row0) = packed;
-                if (mirror) *reinterpret_cast<uint2*>(C + (int64_t)col * g.ldc + row0) = packed;
+                *t = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
             }
         }
+    __syncthreads();
+    if (CT || mirror) {  // rows of C^T: T row c -> row n0 + c
+        uint16_t* __restrict__ dst = CT ? CT : C;
+        const int64_t ld = CT ? g.ldct : g.ldc;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int q = threadIdx.x + TT * i;
+            const int c = q >> 5, r8 = (q & 31) * 8;
+            const uint2* t = reinterpret_cast<const uint2*>(T + c * LDT + r8);
+            const uint2 lo = t[0], hi = t[1];
+            u32x4 v;
+            v.x = lo.x; v.y = lo.y; v.z = hi.x; v.w = hi.y;
+            *reinterpret_cast<u32x4*>(dst + (int64_t)(n0 + c) * ld + m0 + r8) = v;
+        }
+    }
+    // rows of C: lanes 0-31 take 32 consecutive rows of column chunk k, lanes
+    // 32-63 the same rows of chunk k + 1
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        const int q = threadIdx.x + TT * i;
+        const int r = (q & 31) + 32 * (q >> 10), c8 = ((q >> 5) & 31) * 8;
+        const uint16_t* t = T + c8 * LDT + r;
+        uint32_t h[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) h[u] = t[u * LDT];
+        u32x4 v;
+        v.x = h[0] | (h[1] << 16);
+        v.y = h[2] | (h[3] << 16);
+        v.z = h[4] | (h[5] << 16);
+        v.w = h[6] | (h[7] << 16);
+        *reinterpret_cast<u32x4*>(C + (int64_t)(m0 + r) * g.ldc + n0 + c8) = v;
+    }
 }
 
 }  // namespace ns

@@ -104,6 +104,28 @@ def test_batched_gemm_equals_one_matrix_gemm(g, m, n, k, alpha, beta, sym, dt):
     assert torch.equal(other.view(torch.int16), out.transpose(1, 2).contiguous().view(torch.int16))
 
 
+@pytest.mark.parametrize("dt", [False, True])
+def test_batched_gemm_without_transposed_output(dt):
+    """C alone (no C^T, not symmetric), D row-major or given as D^T: bit-identical to
+    the one-matrix kernel."""
+    from gefen_amd.newton_schulz import gemm
+
+    gen = torch.Generator(device="cpu").manual_seed(77 + dt)
+    a = (torch.randn(3, 512, 256, generator=gen) * 0.05).bfloat16().cuda()
+    b = (torch.randn(3, 768, 256, generator=gen) * 0.05).bfloat16().cuda()
+    d = (torch.randn(3, 512, 768, generator=gen) * 0.05).bfloat16().cuda()
+    out = torch.empty(3, 512, 768, dtype=torch.bfloat16, device="cuda:0")
+    if dt:
+        _nt_batched(a, b, out, d_t=d.transpose(1, 2).contiguous(), alpha=0.5, beta=-1.25)
+    else:
+        _nt_batched(a, b, out, d=d, alpha=0.5, beta=-1.25)
+    ref = torch.empty_like(out)
+    for i in range(3):
+        gemm(a[i], b[i], True, ref[i], d=d[i], alpha=0.5, beta=-1.25)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 def test_batched_gemm_rejects_untiled_shapes():
     from gefen_amd import _lib
     from gefen_amd.newton_schulz import gemm_nt_batched
