@@ -193,8 +193,8 @@ __global__ __launch_bounds__(NT) void k_gemm(const uint16_t* __restrict__ A, int
 // (the Gram matrix X X^T, A A with A symmetric, and B X with X^T kept beside X).
 // A 512-thread workgroup owns a 256x256 tile; its eight waves (2 x 4) each own
 // 128x64 as 4x2 v_mfma_f32_32x32x16_bf16 tiles (128 fp32 accumulators per
-// lane).  K moves TK (64) at a time: two register stages and two LDS stages
-// give a prefetch distance of two steps.  Symmetric outputs (X X^T, b A + c A A)
+// lane).  K moves TK (64) at a time through one register stage and two LDS
+// stages (global loads run two steps ahead of the MFMAs that use them).  Symmetric outputs (X X^T, b A + c A A)
 // compute only the tiles on and above the diagonal and mirror them; CT
 // (optional) receives C^T.  Each XCD takes a contiguous run of tiles, in bands
 // of kGroupM tile rows, so workgroups that share operand panels share an L2.
@@ -271,6 +271,7 @@ __device__ __forceinline__ int logical_block(int b, int nwg) {
 // for them, which would cut the prefetch short).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+
 // Epilogue tile in LDS: T[c][r] = C[r][c] (the C^T orientation) in rows of LDT
 // bf16.  LDT / 2 = 130 dwords = 2 (mod 32): the 8-byte accesses of 16
 // consecutive columns cover all 32 banks once, and gathering one row from
@@ -317,20 +318,23 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const int nk = g.K / TK;
-    u32x4 ra0[TCH], rb0[TCH], ra1[TCH], rb1[TCH];  // register stages 0 and 1
-    tile_load(A, g.lda, m0, 0, ra0);
-    tile_load(B, g.ldb, n0, 0, rb0);
+    u32x4 ra[TCH], rb[TCH];  // register stage of the global -> LDS pipeline
+    tile_load(A, g.lda, m0, 0, ra);
+    tile_load(B, g.ldb, n0, 0, rb);
+    tile_store(As[0], ra);
+    tile_store(Bs[0], rb);
     if (nk > 1) {
-        tile_load(A, g.lda, m0, TK, ra1);
-        tile_load(B, g.ldb, n0, TK, rb1);
+        tile_load(A, g.lda, m0, TK, ra);
+        tile_load(B, g.ldb, n0, TK, rb);
     }
-    tile_store(As[0], ra0);
-    tile_store(Bs[0], rb0);
     __syncthreads();
-    // one K step from LDS stage CUR; register stage CUR refills with step kt + 2
-    // (clamped to the last step, so the loads are unconditional and the wait
-    // before the LDS stores leaves exactly those loads in flight).  Fragments
-    // of the next 16-deep slice are read while the current slice's MFMAs run.
+    // One K step from LDS stage CUR.  It first stores step kt + 1 (loaded during
+    // step kt - 1) into the other LDS stage, which every wave finished reading
+    // before the last barrier, then reloads the registers with step kt + 2
+    // (clamped to the last step: the loads are unconditional).  Fragments of the
+    // next 16-deep slice are read while the current slice's MFMAs run.  (A
+    // second register stage, loads two steps ahead with the stores after the
+    // MFMAs, measured 5% slower: the stores then wait at the end of every step.)
 #define GEFEN_LOAD_FRAGS(AS, BS, KK, AF, BF)                                                                      \
     {                                                                                                             \
         _Pragma("unroll") for (int i = 0; i < WI; ++i) AF[i] =                                                    \
@@ -341,11 +345,15 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
 #define GEFEN_MFMAS(AF, BF)                                                                                       \
     _Pragma("unroll") for (int i = 0; i < WI; ++i) _Pragma("unroll") for (int j = 0; j < WJ; ++j) acc[i][j] =     \
         __builtin_amdgcn_mfma_f32_32x32x16_bf16(AF[i], BF[j], acc[i][j], 0, 0, 0);
-#define GEFEN_TILE_STEP(KT, CUR, RA, RB, RA_NEXT, RB_NEXT)                                                       \
+#define GEFEN_TILE_STEP(KT, CUR)                                                                                  \
     {                                                                                                             \
+        if ((KT) + 1 < nk) {                                                                                      \
+            tile_store(As[(CUR) ^ 1], ra);                                                                        \
+            tile_store(Bs[(CUR) ^ 1], rb);                                                                        \
+        }                                                                                                         \
         const int kpre = min((KT) + 2, nk - 1) * TK;                                                              \
-        tile_load(A, g.lda, m0, kpre, RA);                                                                        \
-        tile_load(B, g.ldb, n0, kpre, RB);                                                                        \
+        tile_load(A, g.lda, m0, kpre, ra);                                                                        \
+        tile_load(B, g.ldb, n0, kpre, rb);                                                                        \
         const uint16_t* as = As[CUR];                                                                             \
         const uint16_t* bs = Bs[CUR];                                                                             \
         bf16x8 af0[WI], bf0[WJ], af1[WI], bf1[WJ];                                                                \
@@ -356,18 +364,14 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
             if (kk + 32 < TK) GEFEN_LOAD_FRAGS(as, bs, kk + 32, af0, bf0)                                         \
             GEFEN_MFMAS(af1, bf1)                                                                                 \
         }                                                                                                         \
-        if ((KT) + 1 < nk) {                                                                                      \
-            tile_store(As[(CUR) ^ 1], RA_NEXT);                                                                   \
-            tile_store(Bs[(CUR) ^ 1], RB_NEXT);                                                                   \
-        }                                                                                                         \
         lds_barrier();                                                                                            \
     }
     int kt = 0;
     for (; kt + 1 < nk; kt += 2) {
-        GEFEN_TILE_STEP(kt, 0, ra0, rb0, ra1, rb1)
-        GEFEN_TILE_STEP(kt + 1, 1, ra1, rb1, ra0, rb0)
+        GEFEN_TILE_STEP(kt, 0)
+        GEFEN_TILE_STEP(kt + 1, 1)
     }
-    if (kt < nk) GEFEN_TILE_STEP(kt, 0, ra0, rb0, ra1, rb1)
+    if (kt < nk) GEFEN_TILE_STEP(kt, 0)
 #undef GEFEN_TILE_STEP
 #undef GEFEN_MFMAS
 #undef GEFEN_LOAD_FRAGS
@@ -385,20 +389,24 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     constexpr int kChunks = TM * TN / 8 / TT;  // 16-byte chunks per thread
     const bool d_lds = D && g.d_t;
     if (d_lds) {
-        u32x4 dv[kChunks];
+        constexpr int kBatch = kChunks < 16 ? kChunks : 16;  // loads in flight per thread
 #pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
-            const int q = threadIdx.x + TT * i;
-            const int c = q >> 5, r8 = (q & 31) * 8;
-            dv[i] = *reinterpret_cast<const u32x4*>(D + (int64_t)(n0 + c) * g.ldd + m0 + r8);
-        }
+        for (int i0 = 0; i0 < kChunks; i0 += kBatch) {
+            u32x4 dv[kBatch];
 #pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
-            const int q = threadIdx.x + TT * i;
-            const int c = q >> 5, r8 = (q & 31) * 8;
-            uint2* t = reinterpret_cast<uint2*>(T + c * LDT + r8);
-            t[0] = make_uint2(dv[i].x, dv[i].y);
-            t[1] = make_uint2(dv[i].z, dv[i].w);
+            for (int i = 0; i < kBatch; ++i) {
+                const int q = threadIdx.x + TT * (i0 + i);
+                const int c = q >> 5, r8 = (q & 31) * 8;
+                dv[i] = *reinterpret_cast<const u32x4*>(D + (int64_t)(n0 + c) * g.ldd + m0 + r8);
+            }
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                const int q = threadIdx.x + TT * (i0 + i);
+                const int c = q >> 5, r8 = (q & 31) * 8;
+                uint2* t = reinterpret_cast<uint2*>(T + c * LDT + r8);
+                t[0] = make_uint2(dv[i].x, dv[i].y);
+                t[1] = make_uint2(dv[i].z, dv[i].w);
+            }
         }
         __syncthreads();
     }
