@@ -263,7 +263,8 @@ class _StepPlan:
     (and changes nothing) when the plan no longer applies.
     """
 
-    __slots__ = ("params", "pptr", "numel", "gdtype", "states", "srefs", "groups", "tasks", "device", "dev_index")
+    __slots__ = ("params", "pptr", "numel", "gdtype", "states", "srefs", "groups", "tasks", "device", "dev_index",
+                 "grads", "gptr", "distinct", "group_index", "hyper")
 
     def __init__(self, opt, items, tasks, device):
         self.params = [it[1] for it in items]
@@ -273,56 +274,89 @@ class _StepPlan:
         self.states = [opt.state[it[1]] for it in items]
         self.srefs = [(st["m_codebook"], st["m_magnitude"], st["vmean"]) for st in self.states]
         self.groups = [it[0] for it in items]
+        # position of each tensor's group among the distinct groups (hyperparameters are per group)
+        self.distinct = _distinct(self.groups)
+        self.group_index = [next(i for i, d in enumerate(self.distinct) if d is grp) for grp in self.groups]
         self.tasks = tasks.copy()
         self.device = device
         self.dev_index = device.index if device.index is not None else torch.cuda.current_device()
+        # gradient tensors of the last refresh: the same object again needs no layout checks
+        self.grads = [None] * len(items)
+        self.gptr = [0] * len(items)
+        self.hyper = None  # per-group hyperparameters last written into the table
 
     def refresh(self, opt):
-        params, pptr, numel, gdtype = self.params, self.pptr, self.numel, self.gdtype
+        params, pptr, numel, gdtype, grads, gptr = self.params, self.pptr, self.numel, self.gdtype, self.grads, self.gptr
         n = len(params)
         dev = self.dev_index
-        gptr = []
         k = 0
         for group in opt.param_groups:
             for p in group["params"]:
                 g = p.grad
                 if g is None:
                     continue
-                if k == n or p is not params[k] or type(g) is not torch.Tensor:
+                if k == n or p is not params[k]:
                     return None
-                if (g.dtype is not gdtype[k] or g.numel() != numel[k] or not g.is_contiguous()
-                        or g.get_device() != dev or p.data_ptr() != pptr[k] or not p.is_contiguous()):
+                if g is not grads[k]:
+                    if (type(g) is not torch.Tensor or g.dtype is not gdtype[k] or g.numel() != numel[k]
+                            or not g.is_contiguous() or g.get_device() != dev):
+                        return None
+                    grads[k] = g
+                elif g.numel() != numel[k] or not g.is_contiguous():  # resized or restrided in place
                     return None
-                gptr.append(g.data_ptr())
+                if p.data_ptr() != pptr[k] or not p.is_contiguous():
+                    return None
+                gptr[k] = g.data_ptr()
                 k += 1
         if k != n:
             return None
         for st, (mc, mm, vm) in zip(self.states, self.srefs):
             if st.get("m_codebook") is not mc or st.get("m_magnitude") is not mm or st.get("vmean") is not vm:
                 return None
-        lr, b1s, b2s, eps, wd, bc1, bc2 = [], [], [], [], [], [], []
-        for st, group in zip(self.states, self.groups):
-            st["step"] += 1
-            step = st["step"]
-            glr = group["lr"]
-            lr.append(float(glr.item()) if torch.is_tensor(glr) else float(glr))
-            b1, b2 = group["beta1"], group["beta2"]
-            b1s.append(b1)
-            b2s.append(b2)
-            eps.append(group["eps"])
-            wd.append(group["weight_decay"])
-            bc1.append(1 - b1 ** step)
-            bc2.append(1 - b2 ** step)
+        # hyperparameters once per distinct group (the table's columns are rewritten
+        # only when they change), bias corrections once per (group, step)
+        hyper = []
+        for grp in self.distinct:
+            glr = grp["lr"]
+            hyper.append((float(glr.item()) if torch.is_tensor(glr) else float(glr), grp["beta1"], grp["beta2"],
+                          grp["eps"], grp["weight_decay"]))
         t = self.tasks
+        if hyper != self.hyper:
+            gi = self.group_index
+            for col, j in (("lr", 0), ("beta1", 1), ("beta2", 2), ("eps", 3), ("weight_decay", 4)):
+                t[col] = [hyper[i][j] for i in gi]
+            self.hyper = hyper
+        steps = []
+        for st in self.states:
+            step = st["step"] + 1
+            st["step"] = step
+            steps.append(step)
+        if len(hyper) == 1 and steps[0] == steps[-1] and steps.count(steps[0]) == n:
+            b1, b2 = hyper[0][1], hyper[0][2]
+            t["bias_correction_1"] = 1 - b1 ** steps[0]
+            t["bias_correction_2"] = 1 - b2 ** steps[0]
+        else:
+            corr = {}
+            bc1, bc2 = [], []
+            for gi, step in zip(self.group_index, steps):
+                c = corr.get((gi, step))
+                if c is None:
+                    c = corr[(gi, step)] = (1 - hyper[gi][1] ** step, 1 - hyper[gi][2] ** step)
+                bc1.append(c[0])
+                bc2.append(c[1])
+            t["bias_correction_1"] = bc1
+            t["bias_correction_2"] = bc2
         t["grad"] = gptr
-        t["lr"] = lr
-        t["beta1"] = b1s
-        t["beta2"] = b2s
-        t["eps"] = eps
-        t["weight_decay"] = wd
-        t["bias_correction_1"] = bc1
-        t["bias_correction_2"] = bc2
         return t
+
+
+def _distinct(objs):
+    """The distinct objects of a list by identity, in first-appearance order."""
+    out = []
+    for o in objs:
+        if not any(o is d for d in out):
+            out.append(o)
+    return out
 
 
 # --------------------------------------------------------------------------- optimizer
@@ -708,9 +742,13 @@ class Gefen(torch.optim.Optimizer):
             self._step_all_build()
             return
         lib = _lib.load()
-        with torch.cuda.device(plan.device):
-            rc = lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), self._codebook_tables().data_ptr(),
-                                      torch.cuda.current_stream(plan.device).cuda_stream)
+        tables = self._codebook_tables().data_ptr()
+        if torch.cuda.current_device() == plan.dev_index:
+            rc = lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), tables, torch.cuda.current_stream().cuda_stream)
+        else:
+            with torch.cuda.device(plan.device):
+                rc = lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), tables,
+                                          torch.cuda.current_stream(plan.device).cuda_stream)
         _lib.check(rc, "gefen_step_tasks")
 
     def _step_all_build(self) -> None:
