@@ -24,8 +24,11 @@
 
 namespace gefen {
 
-#ifndef GEFEN_STEP_ITER
-#define GEFEN_STEP_ITER 4
+#ifndef GEFEN_MUON_TAB_LOG2
+#define GEFEN_MUON_TAB_LOG2 6  // GefenMuon row tables for lane groups of 64 lanes
+#endif
+#ifndef GEFEN_MUON_ITER
+#define GEFEN_MUON_ITER 1
 #endif
 #ifndef GEFEN_STEP_ITER_ROWS
 #define GEFEN_STEP_ITER_ROWS 1
@@ -40,7 +43,7 @@ namespace gefen {
 #define GEFEN_STEP_WAVES 4
 #endif
 constexpr int kThreads = 256;  // 4 waves: two-sweep, GefenMuon and vmean kernels
-constexpr int kIter = GEFEN_STEP_ITER;  // wave-units per wave in one GefenMuon workgroup
+constexpr int kMuonIter = GEFEN_MUON_ITER;  // wave-units per wave in one GefenMuon workgroup
 // wave-units per wave in one step workgroup: block rows, period-one rows
 constexpr int kIterRows = GEFEN_STEP_ITER_ROWS;
 constexpr int kIterP1 = GEFEN_STEP_ITER_P1;
@@ -485,91 +488,141 @@ struct MuonBatch {
     const CodebookTables* tables;
 };
 
-template <typename D, typename S>
-__device__ __forceinline__ float muon_out(float q, float gf, const MuonTask& T) {
-    if (!T.nesterov) return q;
-    const float a = round_to<D>(q * T.mom);  // mul_(momentum)
-    if (sizeof(D) == 4) return __builtin_fmaf(gf, T.alpha, a);  // add_(g, alpha): fma
+// Nesterov blend of gefen_muon.py:312-316 on a = D(q * momentum): add_(g, alpha)
+template <typename D>
+__device__ __forceinline__ float muon_blend(float a, float gf, const MuonTask& T) {
+    if (!T.nesterov) return a;
+    if (sizeof(D) == 4) return __builtin_fmaf(gf, T.alpha, a);  // fp32: fma
     return a + gf * T.alpha;  // reduced dtype: alpha in D, exact product, one rounding
 }
 
-template <typename D, typename S, int W, int R>
+template <typename D, typename S>
+__device__ __forceinline__ float muon_out(float q, float gf, const MuonTask& T) {
+    if (!T.nesterov) return q;
+    return muon_blend<D>(round_to<D>(q * T.mom), gf, T);  // mul_(momentum), then the blend
+}
+
+// Register path: as k_gefen_step, a lane group per row and straight-line
+// unconditional loads (a lane group past the last row reads the last row, a
+// vector past the row end the row's last vector: the absmax is idempotent under
+// such copies), non-temporal, addressed from the wave's unit base.  TAB: a lane
+// group of >= 32 lanes keeps two row tables in LDS, cur[i] = D(cb_D[i] * old
+// magnitude) and out[i] = the output of codeword i without the Nesterov
+// gradient term, so the element loops look them up instead of recomputing.
+template <typename D, typename S, int W, int R, bool TAB>
 __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     __shared__ LdsTables L;
+    __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
     int K;
     load_tables<D, kThreads>(L, B.tables, K);
     const int ti = find_task(B.wg_begin, B.ntasks);
     const MuonTask& T = B.t[ti];
+    const bool two_probe = B.tables->max_probe <= 2;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lpr = 1 << T.lpr_log2;
     const int rpw = 64 >> T.lpr_log2;
     const int lir = lane & (lpr - 1);
     const int sub = lane >> T.lpr_log2;
     const int64_t lw = blockIdx.x - B.wg_begin[ti];
-    const D* __restrict__ g = static_cast<const D*>(T.g);
-    uint8_t* __restrict__ idx = T.idx;
-    S* __restrict__ mag = static_cast<S*>(T.mag);
-    D* __restrict__ out = static_cast<D*>(T.out);
+    float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
+    float* otab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
 
-    for (int it = 0; it < kIter; ++it) {
-        const int64_t unit = (lw * kIter + it) * 4 + wave;
-        const int64_t row = unit * rpw + sub;
-        if (unit * rpw >= T.nrows) break;
+    for (int it = 0; it < kMuonIter; ++it) {
+        const int64_t unit = (lw * kMuonIter + it) * 4 + wave;
+        const int64_t row0 = unit * rpw;
+        if (row0 >= T.nrows) break;  // uniform across the wave
+        const int64_t row = row0 + sub;
         const bool active = row < T.nrows;
-        const int64_t base = row * T.rowlen;
+        const int rsub = active ? sub : (int)(T.nrows - 1 - row0);
+        const int64_t ub = row0 * T.rowlen;
+        const D* __restrict__ g = static_cast<const D*>(T.g) + ub;
+        uint8_t* __restrict__ idx = T.idx + ub;
+        D* __restrict__ out = static_cast<D*>(T.out) + ub;
+        S* __restrict__ mag = static_cast<S*>(T.mag) + row0;
+        const uint32_t base = (uint32_t)rsub * (uint32_t)T.rowlen;
         Vec<D, W> gv[R];
         Vec<uint8_t, W> iv[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int v = min(lir + j * lpr, T.nvec - 1);
+            const uint32_t e = base + (uint32_t)(v * W);
+            gv[j] = sload<D, W>(g, e);
+            iv[j] = sload<uint8_t, W>(idx, e);
+        }
+        const float mold = to_f32(mag[rsub]);
+        if (TAB) {
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = lir + t * lpr;
+                if (i < 256) ctab[i] = round_to<D>(L.cbd[i] * mold);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
         float mu[R][W];
         float mx = 0.0f;
-        const float mold = active ? to_f32(mag[row]) : 0.0f;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-            const int v = lir + j * lpr;
-            if (active && v < T.nvec) {
-                const int64_t e = base + (int64_t)v * W;
-                gv[j] = vload<D, W>(g, e);
-                iv[j] = vload<uint8_t, W>(idx, e);
-            }
-        }
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
-            const int v = lir + j * lpr;
-            if (active && v < T.nvec) {
-#pragma unroll
-                for (int w = 0; w < W; ++w) {
-                    const float gf = to_f32(gv[j].v[w]);
-                    const float m0 = round_to<D>(L.cbd[iv[j].v[w]] * mold);         // dequant * mag
-                    const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));  // lerp_
-                    mu[j][w] = m1;
-                    mx = nanmax(mx, fabsf(m1));
-                }
+            for (int w = 0; w < W; ++w) {
+                const float gf = to_f32(gv[j].v[w]);
+                const float m0 = TAB ? ctab[iv[j].v[w]] : round_to<D>(L.cbd[iv[j].v[w]] * mold);  // dequant * mag
+                const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));                   // lerp_
+                mu[j][w] = m1;
+                mx = nanmax(mx, fabsf(m1));
             }
         }
         mx = group_max(mx, lpr);
-        if (!active) continue;
         const S mag_s = from_f32<S>(mx);
-        if (lir == 0) mag[row] = mag_s;
+        if (active && lir == 0) mag[rsub] = mag_s;
         const float ms = to_f32(mag_s);
         const float clamped = (ms < T.tiny) ? T.tiny : ms;  // clamp(min=tiny) in S
+        // FAST: a finite positive magnitude, the division as the float64 product
+        // with the reciprocal (exact, see div_by_block) and the two-probe search
+        const bool fast = two_probe && ms > 0.0f && clamped < __builtin_inff();
+        const double rb = fast ? 1.0 / (double)clamped : 0.0;
+        // output of codeword k before the Nesterov gradient term: q = D(cb_D[k] * mag),
+        // then D(q * momentum) with Nesterov
+        auto out_base = [&](int k) -> float {
+            const float q = round_to<D>(L.cbd[k] * ms);  // copy_(cb[idx]) then mul_(mag)
+            return T.nesterov ? round_to<D>(q * T.mom) : q;
+        };
+        if (TAB) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = lir + t * lpr;
+                if (i < 256) otab[i] = out_base(i);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-            const int v = lir + j * lpr;
-            if (v < T.nvec) {
-                const int64_t e = base + (int64_t)v * W;
-                Vec<uint8_t, W> io;
-                Vec<D, W> oo;
+            Vec<uint8_t, W> io;
+            Vec<D, W> oo;
 #pragma unroll
-                for (int w = 0; w < W; ++w) {
+            for (int w = 0; w < W; ++w) {
+                int k;
+                if (fast) {
+                    k = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
+                } else {
                     float x = round_to<D>(mu[j][w] / clamped);  // div_
                     if (ms <= 0.0f) x = 0.0f;                   // masked_fill_(mag <= 0)
-                    const int k = nearest_fast(x, L.thr, L.bucket, K);
-                    io.v[w] = (uint8_t)k;
-                    const float q = round_to<D>(L.cbd[k] * ms);  // copy_(cb[idx]) then mul_(mag)
-                    oo.v[w] = from_f32<D>(muon_out<D, S>(q, to_f32(gv[j].v[w]), T));
+                    k = nearest_fast(x, L.thr, L.bucket, K);
                 }
-                vstore<uint8_t, W>(idx, e, io);
-                vstore<D, W>(out, e, oo);
+                io.v[w] = (uint8_t)k;
+                const float a = TAB ? otab[k] : out_base(k);
+                oo.v[w] = from_f32<D>(muon_blend<D>(a, to_f32(gv[j].v[w]), T));
+            }
+            const int v = lir + j * lpr;
+            if (active && v < T.nvec) {
+                const uint32_t e = base + (uint32_t)(v * W);
+                sstore<uint8_t, W>(idx, e, io);
+                sstore<D, W>(out, e, oo);
             }
         }
     }
@@ -916,7 +969,8 @@ template <typename D, typename S>
 hipError_t launch_muon(const Key& k, const MuonBatch& b, int grid, hipStream_t st) {
 #define GEFEN_MUON_CASE(WW, RR)                                                                      \
     if (k.W == WW && k.R == RR) {                                                                   \
-        hipLaunchKernelGGL((k_muon<D, S, WW, RR>), dim3(grid), dim3(kThreads), 0, st, b);           \
+        if (k.tab) hipLaunchKernelGGL((k_muon<D, S, WW, RR, true>), dim3(grid), dim3(kThreads), 0, st, b);  \
+        else hipLaunchKernelGGL((k_muon<D, S, WW, RR, false>), dim3(grid), dim3(kThreads), 0, st, b);       \
         return hipGetLastError();                                                                   \
     }
     if (k.R == 0) {
@@ -1298,7 +1352,9 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     const int64_t nvec = rowlen / W;
     const int l2 = lpr_log2_for(nvec);
     const int R = r_bucket(nvec, l2);
-    Key k{in.grad_dtype, in.state_dtype, R == 0 ? 1 : W, R, 0, 0};
+    // row tables pay off for whole-wave rows (measured: 5% faster there, none for 32-lane rows)
+    const int tab = (R != 0 && l2 >= GEFEN_MUON_TAB_LOG2) ? 1 : 0;
+    Key k{in.grad_dtype, in.state_dtype, R == 0 ? 1 : W, R, 0, tab};
     MuonTask& t = out.task;
     memset(&t, 0, sizeof(t));
     t.g = in.grad;
@@ -1331,7 +1387,7 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     t.alpha = round_host(alpha, in.grad_dtype);
     t.tiny = round_host(tiny, in.state_dtype);
     t.nesterov = in.nesterov ? 1 : 0;
-    t.nwg = task_wgs(k, t.nrows, l2, 4, kIter);
+    t.nwg = task_wgs(k, t.nrows, l2, 4, kMuonIter);
     out.key = k;
     return GEFEN_OK;
 }
