@@ -268,3 +268,45 @@ def test_invalid_arguments_raise_value_error():
     task["bias_correction_1"] = 0.0
     with pytest.raises(ValueError, match="bias_correction_1"):
         _lib.check(lib.gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+
+
+@pytest.mark.parametrize("kind", ["dense", "wide", "repeated"])
+@pytest.mark.parametrize("dt,block", [("bf16", 2048), ("bf16", 256), ("f32", 96), ("f32", 1024)])
+def test_muon_momentum_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, block):
+    """GefenMuon momentum through gefen_muon_tasks: general search path, row tables
+    (whole-wave rows) and rows whose magnitude is 0, inf or NaN, bit-exact against
+    the oracle including the Nesterov output."""
+    print("muon case", kind, dt, block, flush=True)
+    cb = _special_codebook(kind)
+    rows = 12
+    n = rows * block
+    idx_np = np.zeros(n, np.uint8)
+    mag_np = np.zeros(rows, orc.NP_STORAGE[dt])
+    idx_dev = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+    mag_dev = torch.zeros(rows, dtype=gu.TORCH[dt], device="cuda:0")
+    tables = _tables(torch.from_numpy(cb).to("cuda:0"))
+    lib = _lib.load()
+    for step in range(1, 4):
+        g = syn.round_to(syn.row_scaled_normal(79, step, rows, block, -14, -4), dt).reshape(-1).copy()
+        if step == 1:
+            g[:block] = 0
+        if step == 2:
+            g[block + 3] = np.float32(np.inf) if dt == "f32" else 0x7F80
+            g[2 * block + 5] = np.float32(np.nan) if dt == "f32" else 0x7FC0
+        g_dev = gu.to_dev(g, dt)
+        out_dev = torch.empty(n, dtype=gu.TORCH[dt], device="cuda:0")
+        task = np.zeros(1, dtype=_lib.MUON_TASK)
+        task["grad"], task["m_codebook"], task["m_magnitude"] = g_dev.data_ptr(), idx_dev.data_ptr(), mag_dev.data_ptr()
+        task["out"], task["numel"], task["block"] = out_dev.data_ptr(), n, block
+        task["grad_dtype"] = task["state_dtype"] = gu.CODE[dt]
+        task["momentum"], task["nesterov"] = 0.95, 1
+        _lib.check(lib.gefen_muon_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+        ref = np.empty(n, dtype=orc.NP_STORAGE[dt])
+        assert orc.lib().orc_muon_momentum(gu.CODE[dt], gu.CODE[dt], orc._ptr(g), orc._ptr(idx_np), orc._ptr(mag_np),
+                                           orc._ptr(ref), n, block, orc._ptr(cb), cb.size, 0.95, 1) == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(gu.to_np(idx_dev), idx_np, err_msg="idx step {}".format(step))
+        np.testing.assert_array_equal(gu.to_np(mag_dev), mag_np, err_msg="mag step {}".format(step))
+        got = gu.to_np(out_dev)
+        both_nan = np.isnan(orc.to_f32(got, dt)) & np.isnan(orc.to_f32(ref, dt))
+        np.testing.assert_array_equal(np.where(both_nan, 0, got), np.where(both_nan, 0, ref), err_msg="out step {}".format(step))
