@@ -1037,12 +1037,20 @@ hipError_t dispatch_packed(int d, int s, const BatchT& b, int64_t rowlen, int64_
 
 bool valid_pair(int d, int s) { return valid_dtype(d) && valid_dtype(s) && (d == s || s == GEFEN_F32); }
 
-// Work of one task in workgroups for its kernel key.
+// Workgroups of one launch: the dispatch's grid size in threads is 32-bit.
+constexpr int64_t kMaxLaunchWgs = 0xFFFFFFFFLL / 256;
+static_assert(kStepThreads <= 256 && kThreads <= 256, "launch cap assumes at most 256 threads per workgroup");
+
+// Work of one task in workgroups for its kernel key; -1 when it exceeds one
+// launch's grid (the caller rejects the tensor).
 int32_t task_wgs(const Key& k, int64_t nrows, int lpr_log2, int waves, int iters) {
-    if (k.R == 0) return (int32_t)nrows;
-    const int64_t rpw = 64 >> lpr_log2;
-    const int64_t units = (nrows + rpw - 1) / rpw;
-    return (int32_t)((units + waves * iters - 1) / (waves * iters));
+    int64_t wgs = nrows;
+    if (k.R != 0) {
+        const int64_t rpw = 64 >> lpr_log2;
+        const int64_t units = (nrows + rpw - 1) / rpw;
+        wgs = (units + waves * iters - 1) / (waves * iters);
+    }
+    return wgs <= kMaxLaunchWgs ? (int32_t)wgs : -1;
 }
 
 struct PendingStep {
@@ -1062,7 +1070,7 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
         int64_t wg = 0;
         for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
             if (done[j] || !(pend[j].key == pend[i].key)) continue;
-            if (wg + pend[j].task.nwg > INT32_MAX) break;
+            if (wg + pend[j].task.nwg > kMaxLaunchWgs) break;
             b.t[n] = pend[j].task;
             b.wg_begin[n] = (int32_t)wg;
             wg += pend[j].task.nwg;
@@ -1124,6 +1132,7 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     t.do_wd = in.weight_decay > 0.0;
     t.wdf = (float)(1.0 - in.lr * in.weight_decay);
     t.nwg = task_wgs(k, t.nrows, l2, kStepWaves, k.p1 ? kIterP1 : kIterRows);
+    if (t.nwg < 0) return fail_inval("tensor of %lld elements is too large for one launch", (long long)n);
     out.key = k;
     return GEFEN_OK;
 }
@@ -1388,6 +1397,7 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     t.tiny = round_host(tiny, in.state_dtype);
     t.nesterov = in.nesterov ? 1 : 0;
     t.nwg = task_wgs(k, t.nrows, l2, 4, kMuonIter);
+    if (t.nwg < 0) return fail_inval("tensor of %lld elements is too large for one launch", (long long)n);
     out.key = k;
     return GEFEN_OK;
 }
@@ -1403,7 +1413,7 @@ int flush_muon(std::vector<PendingMuon>& pend, const CodebookTables* tables, hip
         int64_t wg = 0;
         for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
             if (done[j] || !(pend[j].key == pend[i].key)) continue;
-            if (wg + pend[j].task.nwg > INT32_MAX) break;
+            if (wg + pend[j].task.nwg > kMaxLaunchWgs) break;
             b.t[n] = pend[j].task;
             b.wg_begin[n] = (int32_t)wg;
             wg += pend[j].task.nwg;
