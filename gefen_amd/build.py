@@ -1,4 +1,5 @@
-"""Build libgefen_hip.so (the C-ABI library) and libgefen_synth.so in-tree.
+"""Build libgefen_hip.so (the C-ABI library), libgefen_synth.so and the host
+extension _gefen_host in-tree.
 
     python -m gefen_amd.build [--jobs N]
 
@@ -73,6 +74,33 @@ def build(jobs: int = 8, only=None) -> None:
             sys.stderr.write(r.stdout + r.stderr)
             raise RuntimeError("link failed for {}".format(lib))
         os.replace(tmp, out)
+    if not only or "_gefen_host" in only:
+        build_host_ext()
+
+
+def build_host_ext() -> None:
+    """_gefen_host: the host-side plan checks (csrc/host_plan.cpp), a CPython
+    extension built with the host C++ compiler against torch's headers."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = cpp_extension.library_paths()[0]
+    out = PKG / ("_gefen_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall",
+           "-D_GLIBCXX_USE_CXX11_ABI={}".format(int(torch.compiled_with_cxx11_abi())),
+           "-I", sysconfig.get_paths()["include"]]
+    for inc in cpp_extension.include_paths():
+        cmd += ["-I", inc]
+    cmd += [str(CSRC / "host_plan.cpp"), "-o", str(tmp), "-L", torch_lib, "-Wl,-rpath," + torch_lib,
+            "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("host extension build failed")
+    os.replace(tmp, out)
 
 
 if __name__ == "__main__":
@@ -80,4 +108,4 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=8)
     args = ap.parse_args()
     build(args.jobs)
-    print("built", ", ".join(LIBS))
+    print("built", ", ".join(list(LIBS) + ["_gefen_host"]))

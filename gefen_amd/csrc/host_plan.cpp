@@ -1,0 +1,231 @@
+// Host side of the cached step plan (gefen_amd/gefen.py, _StepPlan.refresh):
+// the per-tensor checks of a steady-state Gefen.step (gefen.py:1399-1420 and
+// the parameter loop of _step_automatic, gefen.py:1208-1333) done in C++ on
+// torch's own tensor objects instead of through ~7 Python attribute calls per
+// tensor.
+//
+// PlanCore holds, for every parameter that had a gradient when the plan was
+// built (in optimizer order): the parameter object, its data pointer, the
+// gradient's element count and dtype, the parameter's state dict and the three
+// state tensor objects.  refresh() walks the optimizer's param groups and
+// succeeds only if the parameters with a gradient are exactly those objects in
+// that order, every gradient is a plain (no Python dispatch) strided contiguous
+// tensor of the recorded dtype, size and device, every parameter keeps its data
+// pointer and is contiguous, and every state dict still holds the same state
+// tensors and an int "step".  Only then does it write each task row's gradient
+// address, group hyperparameters and bias corrections and advance every
+// state["step"]; on any mismatch it changes nothing and returns false (the
+// caller rebuilds the plan).
+//
+// Built with the host compiler against torch's headers (no device code).
+
+#include <Python.h>
+#include <pybind11/pybind11.h>
+#include <torch/csrc/autograd/python_variable.h>
+
+#include <array>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+namespace py = pybind11;
+
+namespace {
+
+// interned dict keys, created once at module import
+PyObject* key_params_;
+PyObject* key_step_;
+PyObject* key_m_codebook_;
+PyObject* key_m_magnitude_;
+PyObject* key_vmean_;
+PyObject* key_lr_;
+PyObject* key_beta1_;
+PyObject* key_beta2_;
+PyObject* key_eps_;
+PyObject* key_wd_;
+
+PyObject* intern(const char* s) {
+    PyObject* k = PyUnicode_InternFromString(s);
+    if (!k) throw py::error_already_set();
+    return k;
+}
+
+class PlanCore {
+   public:
+    // params: the parameters with a gradient, in optimizer order (their current
+    // gradients give the recorded size, dtype and device); states: their state
+    // dicts; state_tensors: (m_codebook, m_magnitude, vmean) of each.
+    PlanCore(py::list params, py::list states, py::list state_tensors) {
+        const size_t n = params.size();
+        if (states.size() != n || state_tensors.size() != n)
+            throw py::value_error("PlanCore: lists of different lengths");
+        for (size_t k = 0; k < n; ++k) {
+            py::handle p = params[k];
+            if (!THPVariable_Check(p.ptr())) throw py::type_error("PlanCore: parameter is not a tensor");
+            const at::Tensor& t = THPVariable_Unpack(p.ptr());
+            const at::Tensor& g = t.grad();
+            if (!g.defined()) throw py::value_error("PlanCore: parameter without a gradient");
+            if (k == 0) {
+                device_type_ = static_cast<int>(g.device().type());
+                device_index_ = g.device().index();
+            }
+            params_.push_back(py::reinterpret_borrow<py::object>(p));
+            pptr_.push_back(reinterpret_cast<uintptr_t>(t.data_ptr()));
+            numel_.push_back(g.numel());
+            dtype_.push_back(g.scalar_type());
+            py::handle st = states[k];
+            if (!PyDict_Check(st.ptr())) throw py::type_error("PlanCore: state is not a dict");
+            states_.push_back(py::reinterpret_borrow<py::object>(st));
+            py::tuple refs = py::reinterpret_borrow<py::tuple>(state_tensors[k]);
+            if (refs.size() != 3) throw py::value_error("PlanCore: three state tensors per parameter");
+            srefs_.push_back({py::reinterpret_borrow<py::object>(refs[0]), py::reinterpret_borrow<py::object>(refs[1]),
+                              py::reinterpret_borrow<py::object>(refs[2])});
+        }
+        gptr_.resize(n);
+        step_.resize(n);
+        hyper_.resize(n);
+    }
+
+    // table: address of the task table (rows of `stride` bytes); cols: byte offsets
+    // within a row of grad, lr, beta1, beta2, eps, weight_decay, bias_correction_1,
+    // bias_correction_2 (uint64 address, then doubles); steps_out: n int64 slots
+    // receiving the advanced step counts.  Hyperparameters come from each
+    // parameter's group (lr may be a 0-d tensor); the bias corrections are
+    // 1 - beta ** step in double, as Python evaluates them (gefen.py:1278-1284).
+    bool refresh(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols, uintptr_t steps_out) {
+        if (!PyList_Check(param_groups.ptr()) || cols.size() != 8) return false;
+        size_t col[8];
+        for (int i = 0; i < 8; ++i) col[i] = cols[i].cast<size_t>();
+        const size_t n = params_.size();
+        size_t k = 0;
+        const Py_ssize_t ngroups = PyList_GET_SIZE(param_groups.ptr());
+        for (Py_ssize_t gi = 0; gi < ngroups; ++gi) {
+            PyObject* group = PyList_GET_ITEM(param_groups.ptr(), gi);
+            if (!PyDict_Check(group)) return false;
+            PyObject* plist = PyDict_GetItem(group, key_params_);
+            if (!plist || !PyList_Check(plist)) return false;
+            const Py_ssize_t np = PyList_GET_SIZE(plist);
+            bool have_hyper = false;
+            std::array<double, 5> h{};
+            for (Py_ssize_t i = 0; i < np; ++i) {
+                PyObject* p = PyList_GET_ITEM(plist, i);
+                if (!THPVariable_Check(p)) return false;
+                const at::Tensor& t = THPVariable_Unpack(p);
+                const at::Tensor& g = t.grad();
+                if (!g.defined()) continue;
+                if (k == n || p != params_[k].ptr()) return false;
+                if (g.key_set().has(c10::DispatchKey::Python) || g.layout() != at::kStrided ||
+                    g.scalar_type() != dtype_[k] || g.numel() != numel_[k] || !g.is_contiguous() ||
+                    static_cast<int>(g.device().type()) != device_type_ || g.device().index() != device_index_)
+                    return false;
+                if (reinterpret_cast<uintptr_t>(t.data_ptr()) != pptr_[k] || !t.is_contiguous()) return false;
+                if (!have_hyper) {
+                    if (!group_hyper(group, h)) return false;
+                    have_hyper = true;
+                }
+                gptr_[k] = reinterpret_cast<uint64_t>(g.data_ptr());
+                hyper_[k] = h;
+                ++k;
+            }
+        }
+        if (k != n) return false;
+        for (k = 0; k < n; ++k) {
+            PyObject* st = states_[k].ptr();
+            if (PyDict_GetItem(st, key_m_codebook_) != srefs_[k][0].ptr() ||
+                PyDict_GetItem(st, key_m_magnitude_) != srefs_[k][1].ptr() ||
+                PyDict_GetItem(st, key_vmean_) != srefs_[k][2].ptr())
+                return false;
+            PyObject* s = PyDict_GetItem(st, key_step_);
+            if (!s || !PyLong_CheckExact(s)) return false;
+            const long long v = PyLong_AsLongLong(s);
+            if (v == -1 && PyErr_Occurred()) {
+                PyErr_Clear();
+                return false;
+            }
+            step_[k] = v + 1;
+        }
+        // every check passed: commit
+        int64_t* steps = reinterpret_cast<int64_t*>(steps_out);
+        double last_b1 = 0.0, last_b2 = 0.0, bc1 = 0.0, bc2 = 0.0;
+        long long last_step = -1;
+        for (k = 0; k < n; ++k) {
+            char* row = reinterpret_cast<char*>(table + k * stride);
+            const std::array<double, 5>& h = hyper_[k];
+            if (step_[k] != last_step || h[1] != last_b1 || h[2] != last_b2) {
+                bc1 = 1.0 - std::pow(h[1], (double)step_[k]);
+                bc2 = 1.0 - std::pow(h[2], (double)step_[k]);
+                last_step = step_[k];
+                last_b1 = h[1];
+                last_b2 = h[2];
+            }
+            const uint64_t gp = gptr_[k];
+            std::memcpy(row + col[0], &gp, 8);
+            for (int c = 0; c < 5; ++c) std::memcpy(row + col[1 + c], &h[c], 8);
+            std::memcpy(row + col[6], &bc1, 8);
+            std::memcpy(row + col[7], &bc2, 8);
+            PyObject* v = PyLong_FromLongLong(step_[k]);
+            if (!v) throw py::error_already_set();
+            const int rc = PyDict_SetItem(states_[k].ptr(), key_step_, v);
+            Py_DECREF(v);
+            if (rc != 0) throw py::error_already_set();
+            steps[k] = step_[k];
+        }
+        return true;
+    }
+
+    size_t size() const { return params_.size(); }
+
+   private:
+    // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group
+    bool group_hyper(PyObject* group, std::array<double, 5>& h) {
+        PyObject* keys[5] = {key_lr_, key_beta1_, key_beta2_, key_eps_, key_wd_};
+        for (int c = 0; c < 5; ++c) {
+            PyObject* v = PyDict_GetItem(group, keys[c]);
+            if (!v) return false;
+            if (PyFloat_CheckExact(v)) {
+                h[c] = PyFloat_AS_DOUBLE(v);
+                continue;
+            }
+            PyObject* f = PyNumber_Float(v);  // ints, numpy scalars, 0-d tensors (.item())
+            if (!f) {
+                PyErr_Clear();
+                return false;
+            }
+            h[c] = PyFloat_AS_DOUBLE(f);
+            Py_DECREF(f);
+        }
+        return true;
+    }
+
+    int device_type_ = -1, device_index_ = -1;
+    std::vector<py::object> params_;
+    std::vector<uintptr_t> pptr_;
+    std::vector<int64_t> numel_;
+    std::vector<at::ScalarType> dtype_;
+    std::vector<py::object> states_;
+    std::vector<std::array<py::object, 3>> srefs_;
+    std::vector<uint64_t> gptr_;
+    std::vector<long long> step_;
+    std::vector<std::array<double, 5>> hyper_;
+};
+
+}  // namespace
+
+PYBIND11_MODULE(_gefen_host, m) {
+    m.doc() = "Host-side checks of the cached Gefen step plan";
+    key_params_ = intern("params");
+    key_step_ = intern("step");
+    key_m_codebook_ = intern("m_codebook");
+    key_m_magnitude_ = intern("m_magnitude");
+    key_vmean_ = intern("vmean");
+    key_lr_ = intern("lr");
+    key_beta1_ = intern("beta1");
+    key_beta2_ = intern("beta2");
+    key_eps_ = intern("eps");
+    key_wd_ = intern("weight_decay");
+    py::class_<PlanCore>(m, "PlanCore")
+        .def(py::init<py::list, py::list, py::list>())
+        .def("refresh", &PlanCore::refresh)
+        .def("__len__", &PlanCore::size);
+}

@@ -36,6 +36,9 @@ namespace gefen {
 #ifndef GEFEN_STEP_ITER_P1
 #define GEFEN_STEP_ITER_P1 2
 #endif
+#ifndef GEFEN_STEP_P1_LUT
+#define GEFEN_STEP_P1_LUT 1  // period one, 16-bit state: stepsize from the table (0: computed)
+#endif
 #ifndef GEFEN_STEP_NT
 #define GEFEN_STEP_NT 1
 #endif
@@ -160,7 +163,7 @@ template <typename S>
 __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
     if constexpr (sizeof(S) == 2) {
         const uint16_t bits = reinterpret_cast<const uint16_t&>(v);
-        if (T.lut && !(bits & 0x8000u)) return T.lut[bits];
+        if (GEFEN_STEP_P1_LUT && T.lut && !(bits & 0x8000u)) return T.lut[bits];
     }
     return stepsize_of(to_f32(v), T);
 }

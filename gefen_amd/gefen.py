@@ -30,6 +30,11 @@ import torch.nn as nn
 
 from gefen_amd import _lib
 from gefen_amd import quantization as quantization_module
+
+try:  # host-side plan checks in C++ (gefen_amd/csrc/host_plan.cpp); the Python checks otherwise
+    from gefen_amd import _gefen_host
+except ImportError:
+    _gefen_host = None
 from gefen_amd.partitioning import PeriodScorer, divisors
 
 FIND_PERIOD_BACKEND = None
@@ -264,7 +269,7 @@ class _StepPlan:
     """
 
     __slots__ = ("params", "pptr", "numel", "gdtype", "states", "srefs", "groups", "tasks", "device", "dev_index",
-                 "grads", "gptr", "distinct", "group_index", "hyper")
+                 "grads", "gptr", "distinct", "group_index", "hyper", "core", "steps", "columns")
 
     def __init__(self, opt, items, tasks, device):
         self.params = [it[1] for it in items]
@@ -280,12 +285,64 @@ class _StepPlan:
         self.tasks = tasks.copy()
         self.device = device
         self.dev_index = device.index if device.index is not None else torch.cuda.current_device()
-        # gradient tensors of the last refresh: the same object again needs no layout checks
+        # gradient tensors of the last Python refresh: the same object again needs fewer checks
         self.grads = [None] * len(items)
         self.gptr = [0] * len(items)
         self.hyper = None  # per-group hyperparameters last written into the table
+        self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.srefs)
+        self.steps = np.zeros(len(items), dtype=np.int64)
+        fields = self.tasks.dtype.fields
+        self.columns = tuple(fields[c][1] for c in ("grad", "lr", "beta1", "beta2", "eps", "weight_decay",
+                                                     "bias_correction_1", "bias_correction_2"))
 
     def refresh(self, opt):
+        t = self.tasks
+        if self.core is not None:
+            # checks, gradient addresses, hyperparameters, bias corrections and the
+            # step counts in C++ (gefen_amd/csrc/host_plan.cpp)
+            if not self.core.refresh(opt.param_groups, t.ctypes.data, t.itemsize, self.columns,
+                                     self.steps.ctypes.data):
+                return None
+            return t
+        steps = self._refresh_python(opt)
+        if steps is None:
+            return None
+        # hyperparameters once per distinct group (the table's columns are rewritten
+        # only when they change), bias corrections once per (group, step)
+        hyper = []
+        for grp in self.distinct:
+            glr = grp["lr"]
+            hyper.append((float(glr.item()) if torch.is_tensor(glr) else float(glr), grp["beta1"], grp["beta2"],
+                          grp["eps"], grp["weight_decay"]))
+        t = self.tasks
+        if hyper != self.hyper:
+            gi = self.group_index
+            for col, j in (("lr", 0), ("beta1", 1), ("beta2", 2), ("eps", 3), ("weight_decay", 4)):
+                t[col] = [hyper[i][j] for i in gi]
+            self.hyper = hyper
+        if not isinstance(steps, np.ndarray):
+            steps = np.asarray(steps, dtype=np.int64)
+        s0 = int(steps[0])
+        if len(hyper) == 1 and int(steps.min()) == s0 == int(steps.max()):
+            b1, b2 = hyper[0][1], hyper[0][2]
+            t["bias_correction_1"] = 1 - b1 ** s0
+            t["bias_correction_2"] = 1 - b2 ** s0
+        else:
+            corr = {}
+            bc1, bc2 = [], []
+            for gi, step in zip(self.group_index, steps.tolist()):
+                c = corr.get((gi, step))
+                if c is None:
+                    c = corr[(gi, step)] = (1 - hyper[gi][1] ** step, 1 - hyper[gi][2] ** step)
+                bc1.append(c[0])
+                bc2.append(c[1])
+            t["bias_correction_1"] = bc1
+            t["bias_correction_2"] = bc2
+        return t
+
+    def _refresh_python(self, opt):
+        """The checks of PlanCore.refresh in Python (used when the host extension
+        is not built): returns the advanced step counts, or None."""
         params, pptr, numel, gdtype, grads, gptr = self.params, self.pptr, self.numel, self.gdtype, self.grads, self.gptr
         n = len(params)
         dev = self.dev_index
@@ -313,40 +370,15 @@ class _StepPlan:
         for st, (mc, mm, vm) in zip(self.states, self.srefs):
             if st.get("m_codebook") is not mc or st.get("m_magnitude") is not mm or st.get("vmean") is not vm:
                 return None
-        # hyperparameters once per distinct group (the table's columns are rewritten
-        # only when they change), bias corrections once per (group, step)
-        hyper = []
-        for grp in self.distinct:
-            glr = grp["lr"]
-            hyper.append((float(glr.item()) if torch.is_tensor(glr) else float(glr), grp["beta1"], grp["beta2"],
-                          grp["eps"], grp["weight_decay"]))
-        t = self.tasks
-        if hyper != self.hyper:
-            gi = self.group_index
-            for col, j in (("lr", 0), ("beta1", 1), ("beta2", 2), ("eps", 3), ("weight_decay", 4)):
-                t[col] = [hyper[i][j] for i in gi]
-            self.hyper = hyper
+            if type(st.get("step")) is not int:
+                return None
         steps = []
         for st in self.states:
             step = st["step"] + 1
             st["step"] = step
             steps.append(step)
-        if len(hyper) == 1 and steps[0] == steps[-1] and steps.count(steps[0]) == n:
-            b1, b2 = hyper[0][1], hyper[0][2]
-            t["bias_correction_1"] = 1 - b1 ** steps[0]
-            t["bias_correction_2"] = 1 - b2 ** steps[0]
-        else:
-            corr = {}
-            bc1, bc2 = [], []
-            for gi, step in zip(self.group_index, steps):
-                c = corr.get((gi, step))
-                if c is None:
-                    c = corr[(gi, step)] = (1 - hyper[gi][1] ** step, 1 - hyper[gi][2] ** step)
-                bc1.append(c[0])
-                bc2.append(c[1])
-            t["bias_correction_1"] = bc1
-            t["bias_correction_2"] = bc2
-        t["grad"] = gptr
+        self.tasks["grad"] = gptr
+        return steps
         return t
 
 

@@ -134,3 +134,68 @@ def test_step_on_cpu_tensors_fails_loudly():
     opt = Gefen([w])
     with pytest.raises((RuntimeError, ValueError), match="HIP"):
         opt.step()
+
+
+def test_plan_core_checks_and_commits_only_when_the_plan_applies():
+    """PlanCore.refresh (gefen_amd/csrc/host_plan.cpp) on CPU tensors: it fills each
+    task row (gradient address, group hyperparameters, bias corrections 1 - beta **
+    step as Python computes them) and advances the steps only when every parameter
+    with a gradient is the recorded one with a gradient of the recorded layout and
+    the state tensors are unchanged; any mismatch leaves table and steps alone."""
+    import numpy as np
+    import torch
+
+    from gefen_amd import _gefen_host, _lib
+
+    ps = [torch.nn.Parameter(torch.zeros(n)) for n in (8, 16, 4)]
+    for p in ps:
+        p.grad = torch.ones_like(p)
+    states = [{"step": 3, "m_codebook": torch.zeros(1), "m_magnitude": torch.zeros(1), "vmean": torch.zeros(1)}
+              for _ in ps]
+    srefs = [(st["m_codebook"], st["m_magnitude"], st["vmean"]) for st in states]
+    core = _gefen_host.PlanCore(list(ps), states, srefs)
+    assert len(core) == 3
+    groups = [{"params": [ps[0], ps[1]], "lr": 1e-3, "beta1": 0.9, "beta2": 0.999, "eps": 1e-8, "weight_decay": 0},
+              {"params": [ps[2]], "lr": torch.tensor(2e-3, dtype=torch.float64), "beta1": 0.8, "beta2": 0.99,
+               "eps": 1e-6, "weight_decay": 0.1}]
+    table = np.zeros(3, dtype=_lib.STEP_TASK)
+    steps = np.zeros(3, dtype=np.int64)
+    cols = tuple(table.dtype.fields[c][1] for c in ("grad", "lr", "beta1", "beta2", "eps", "weight_decay",
+                                                     "bias_correction_1", "bias_correction_2"))
+
+    def refresh(gr):
+        return core.refresh(gr, table.ctypes.data, table.itemsize, cols, steps.ctypes.data)
+
+    assert refresh(groups)
+    assert table["grad"].tolist() == [p.grad.data_ptr() for p in ps]
+    assert steps.tolist() == [4, 4, 4] and [st["step"] for st in states] == [4, 4, 4]
+    assert table["lr"].tolist() == [1e-3, 1e-3, 2e-3] and table["weight_decay"].tolist() == [0.0, 0.0, 0.1]
+    assert table["beta1"].tolist() == [0.9, 0.9, 0.8] and table["eps"].tolist() == [1e-8, 1e-8, 1e-6]
+    assert table["bias_correction_1"].tolist() == [1 - 0.9 ** 4, 1 - 0.9 ** 4, 1 - 0.8 ** 4]
+    assert table["bias_correction_2"].tolist() == [1 - 0.999 ** 4, 1 - 0.999 ** 4, 1 - 0.99 ** 4]
+
+    def unchanged_after(mutate, undo):
+        table["grad"] = 0
+        table["lr"] = 0.0
+        mutate()
+        before = [st["step"] for st in states]
+        assert not refresh(groups)
+        assert table["grad"].tolist() == [0, 0, 0] and table["lr"].tolist() == [0.0, 0.0, 0.0]
+        assert [st["step"] for st in states] == before
+        undo()
+        assert refresh(groups)
+
+    g1 = ps[1].grad
+    unchanged_after(lambda: g1.resize_(12), lambda: g1.resize_(16))  # resized in place
+    unchanged_after(lambda: setattr(ps[1], "grad", torch.ones(32)[::2]), lambda: setattr(ps[1], "grad", g1))
+    unchanged_after(lambda: setattr(ps[1], "grad", None), lambda: setattr(ps[1], "grad", g1))
+    unchanged_after(lambda: groups[0]["params"].reverse(), lambda: groups[0]["params"].reverse())
+    extra = torch.nn.Parameter(torch.zeros(2))
+    extra.grad = torch.ones(2)
+    unchanged_after(lambda: groups[1]["params"].append(extra), lambda: groups[1]["params"].pop())
+    vm = states[2]["vmean"]
+    unchanged_after(lambda: states[2].__setitem__("vmean", vm.clone()), lambda: states[2].__setitem__("vmean", vm))
+    unchanged_after(lambda: states[0].__setitem__("step", torch.tensor(5)), lambda: states[0].__setitem__("step", 9))
+    unchanged_after(lambda: groups[1].__setitem__("lr", "fast"), lambda: groups[1].__setitem__("lr", 2e-3))
+    assert [st["step"] for st in states] == [11, 12, 12] and steps.tolist() == [11, 12, 12]
+    assert table["bias_correction_1"].tolist() == [1 - 0.9 ** 11, 1 - 0.9 ** 12, 1 - 0.8 ** 12]

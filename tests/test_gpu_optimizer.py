@@ -160,12 +160,20 @@ def test_gefen_muon_matches_reference_trajectory(name):
                 assert rel <= tol, "{} p{} step {}: relative update error {:.3g}".format(name, i, step, rel)
 
 
-def test_cached_step_plan_matches_rebuilt_task_table():
+@pytest.mark.parametrize("host_checks", ["c++", "python"])
+def test_cached_step_plan_matches_rebuilt_task_table(host_checks, monkeypatch):
     """Steps through the cached plan equal steps that rebuild the task table from
     scratch, bit for bit, across the events that invalidate the plan: an lr
     change, a skipped gradient, a non-contiguous gradient, load_state_dict and
-    a weight-decay change."""
+    a weight-decay change; with the plan checks in the host extension and in
+    Python."""
+    from gefen_amd import gefen as gefen_mod
     from gefen_amd.gefen import Gefen
+
+    if host_checks == "c++":
+        assert gefen_mod._gefen_host is not None, "host extension not built"
+    else:
+        monkeypatch.setattr(gefen_mod, "_gefen_host", None)
 
     shapes = [(64, 96), (96,), (32, 48), (128, 256)]
 
