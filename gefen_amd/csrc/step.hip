@@ -66,7 +66,7 @@ __device__ __forceinline__ void sstore(T* base, uint32_t elem, const Vec<T, W>& 
     if constexpr (kStreamNT) vstore32_nt<T, W>(base, elem, x);
     else vstore32<T, W>(base, elem, x);
 }
-constexpr int kMaxBatch = 20;  // tasks per launch (kernel argument block < 4 KB)
+constexpr int kMaxBatch = 30;  // tasks per launch (the task table is the kernel argument block, < 4 KB)
 
 enum StepMode : int32_t { kVmeanUpdate = 0, kVmeanGiven = 1, kStepsizeGiven = 2 };
 
@@ -96,6 +96,7 @@ struct StepBatch {
     int32_t pad;
     const CodebookTables* tables;
 };
+static_assert(sizeof(StepBatch) <= 4000, "kernel arguments are limited to 4 KB");
 
 // LDS copy of the codebook tables (6 KB): the codebook rounded to the parameter
 // dtype, the thresholds and the byte bucket index.
@@ -143,11 +144,17 @@ __device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* 
     __syncthreads();
 }
 
+// Task of this workgroup: the last t with wg_begin[t] <= blockIdx.x (binary
+// search over the launch's task table; wg_begin[0] = 0 and is non-decreasing).
 __device__ __forceinline__ int find_task(const int32_t* wg_begin, int ntasks) {
-    int t = 0;
     const int b = blockIdx.x;
-    while (t + 1 < ntasks && wg_begin[t + 1] <= b) ++t;
-    return t;
+    int lo = 0, hi = ntasks - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (wg_begin[mid] <= b) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
 }
 
 // stepsize of gefen.py:1326-1327: (1/bc1) * reciprocal(sqrt(v)/sqrt(bc2) + eps)
@@ -490,6 +497,7 @@ struct MuonBatch {
     int32_t pad;
     const CodebookTables* tables;
 };
+static_assert(sizeof(MuonBatch) <= 4000, "kernel arguments are limited to 4 KB");
 
 // Nesterov blend of gefen_muon.py:312-316 on a = D(q * momentum): add_(g, alpha)
 template <typename D>

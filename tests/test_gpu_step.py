@@ -217,11 +217,12 @@ def test_misaligned_views_take_the_scalar_path():
 
 
 def test_many_tasks_in_one_call():
-    """Tensors of mixed dtypes and periods in one gefen_step_tasks call (several launches)."""
+    """Tensors of mixed dtypes and periods in one gefen_step_tasks call: 36 tasks of each
+    kernel shape, so each shape takes more than one launch (at most 30 tasks per launch)."""
     cb = _codebook()
     cb_dev = torch.from_numpy(cb).to("cuda:0")
     tables = _tables(cb_dev)
-    specs = [("bf16", 2048 * 3, 2048), ("bf16", 1024, 1), ("f32", 96 * 10, 96), ("bf16", 768 * 4, 768)] * 12
+    specs = [("bf16", 2048 * 3, 2048), ("bf16", 1024, 1), ("f32", 96 * 10, 96), ("bf16", 768 * 4, 768)] * 36
     tasks = np.zeros(len(specs), dtype=_lib.STEP_TASK)
     devs, oracle = [], []
     for i, (dt, n, period) in enumerate(specs):
