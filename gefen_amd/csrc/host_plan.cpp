@@ -6,8 +6,8 @@
 //
 // PlanCore holds, for every parameter that had a gradient when the plan was
 // built (in optimizer order): the parameter object, its data pointer, the
-// gradient's element count and dtype, the parameter's state dict and the three
-// state tensor objects.  refresh() walks the optimizer's param groups and
+// gradient's element count and dtype, the parameter's state dict and its state
+// tensor objects (the given state keys).  refresh() walks the optimizer's param groups and
 // succeeds only if the parameters with a gradient are exactly those objects in
 // that order, every gradient is a plain (no Python dispatch) strided contiguous
 // tensor of the recorded dtype, size and device, every parameter keeps its data
@@ -36,9 +36,6 @@ namespace {
 // interned dict keys, created once at module import
 PyObject* key_params_;
 PyObject* key_step_;
-PyObject* key_m_codebook_;
-PyObject* key_m_magnitude_;
-PyObject* key_vmean_;
 PyObject* key_lr_;
 PyObject* key_beta1_;
 PyObject* key_beta2_;
@@ -55,11 +52,15 @@ class PlanCore {
    public:
     // params: the parameters with a gradient, in optimizer order (their current
     // gradients give the recorded size, dtype and device); states: their state
-    // dicts; state_tensors: (m_codebook, m_magnitude, vmean) of each.
-    PlanCore(py::list params, py::list states, py::list state_tensors) {
+    // dicts; state_keys: the state entries that must stay the same objects (their
+    // current values are recorded).
+    PlanCore(py::list params, py::list states, py::tuple state_keys) {
         const size_t n = params.size();
-        if (states.size() != n || state_tensors.size() != n)
-            throw py::value_error("PlanCore: lists of different lengths");
+        if (states.size() != n) throw py::value_error("PlanCore: lists of different lengths");
+        for (py::handle key : state_keys) {
+            if (!PyUnicode_Check(key.ptr())) throw py::type_error("PlanCore: state keys are strings");
+            skeys_.push_back(py::reinterpret_borrow<py::object>(key));
+        }
         for (size_t k = 0; k < n; ++k) {
             py::handle p = params[k];
             if (!THPVariable_Check(p.ptr())) throw py::type_error("PlanCore: parameter is not a tensor");
@@ -77,10 +78,13 @@ class PlanCore {
             py::handle st = states[k];
             if (!PyDict_Check(st.ptr())) throw py::type_error("PlanCore: state is not a dict");
             states_.push_back(py::reinterpret_borrow<py::object>(st));
-            py::tuple refs = py::reinterpret_borrow<py::tuple>(state_tensors[k]);
-            if (refs.size() != 3) throw py::value_error("PlanCore: three state tensors per parameter");
-            srefs_.push_back({py::reinterpret_borrow<py::object>(refs[0]), py::reinterpret_borrow<py::object>(refs[1]),
-                              py::reinterpret_borrow<py::object>(refs[2])});
+            std::vector<py::object> refs;
+            for (const py::object& key : skeys_) {
+                PyObject* v = PyDict_GetItem(st.ptr(), key.ptr());
+                if (!v) throw py::key_error("PlanCore: state entry missing");
+                refs.push_back(py::reinterpret_borrow<py::object>(v));
+            }
+            srefs_.push_back(std::move(refs));
         }
         gptr_.resize(n);
         step_.resize(n);
@@ -93,10 +97,14 @@ class PlanCore {
     // receiving the advanced step counts.  Hyperparameters come from each
     // parameter's group (lr may be a 0-d tensor); the bias corrections are
     // 1 - beta ** step in double, as Python evaluates them (gefen.py:1278-1284).
+    //
+    // With cols = (grad,) only the gradient addresses and the step counts are
+    // written (the caller handles the hyperparameters).
     bool refresh(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols, uintptr_t steps_out) {
-        if (!PyList_Check(param_groups.ptr()) || cols.size() != 8) return false;
-        size_t col[8];
-        for (int i = 0; i < 8; ++i) col[i] = cols[i].cast<size_t>();
+        if (!PyList_Check(param_groups.ptr()) || (cols.size() != 8 && cols.size() != 1)) return false;
+        const bool hyper = cols.size() == 8;
+        size_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (size_t i = 0; i < cols.size(); ++i) col[i] = cols[i].cast<size_t>();
         const size_t n = params_.size();
         size_t k = 0;
         const Py_ssize_t ngroups = PyList_GET_SIZE(param_groups.ptr());
@@ -120,7 +128,7 @@ class PlanCore {
                     static_cast<int>(g.device().type()) != device_type_ || g.device().index() != device_index_)
                     return false;
                 if (reinterpret_cast<uintptr_t>(t.data_ptr()) != pptr_[k] || !t.is_contiguous()) return false;
-                if (!have_hyper) {
+                if (hyper && !have_hyper) {
                     if (!group_hyper(group, h)) return false;
                     have_hyper = true;
                 }
@@ -132,10 +140,8 @@ class PlanCore {
         if (k != n) return false;
         for (k = 0; k < n; ++k) {
             PyObject* st = states_[k].ptr();
-            if (PyDict_GetItem(st, key_m_codebook_) != srefs_[k][0].ptr() ||
-                PyDict_GetItem(st, key_m_magnitude_) != srefs_[k][1].ptr() ||
-                PyDict_GetItem(st, key_vmean_) != srefs_[k][2].ptr())
-                return false;
+            for (size_t j = 0; j < skeys_.size(); ++j)
+                if (PyDict_GetItem(st, skeys_[j].ptr()) != srefs_[k][j].ptr()) return false;
             PyObject* s = PyDict_GetItem(st, key_step_);
             if (!s || !PyLong_CheckExact(s)) return false;
             const long long v = PyLong_AsLongLong(s);
@@ -151,19 +157,21 @@ class PlanCore {
         long long last_step = -1;
         for (k = 0; k < n; ++k) {
             char* row = reinterpret_cast<char*>(table + k * stride);
-            const std::array<double, 5>& h = hyper_[k];
-            if (step_[k] != last_step || h[1] != last_b1 || h[2] != last_b2) {
-                bc1 = 1.0 - std::pow(h[1], (double)step_[k]);
-                bc2 = 1.0 - std::pow(h[2], (double)step_[k]);
-                last_step = step_[k];
-                last_b1 = h[1];
-                last_b2 = h[2];
-            }
             const uint64_t gp = gptr_[k];
             std::memcpy(row + col[0], &gp, 8);
-            for (int c = 0; c < 5; ++c) std::memcpy(row + col[1 + c], &h[c], 8);
-            std::memcpy(row + col[6], &bc1, 8);
-            std::memcpy(row + col[7], &bc2, 8);
+            if (hyper) {
+                const std::array<double, 5>& h = hyper_[k];
+                if (step_[k] != last_step || h[1] != last_b1 || h[2] != last_b2) {
+                    bc1 = 1.0 - std::pow(h[1], (double)step_[k]);
+                    bc2 = 1.0 - std::pow(h[2], (double)step_[k]);
+                    last_step = step_[k];
+                    last_b1 = h[1];
+                    last_b2 = h[2];
+                }
+                for (int c = 0; c < 5; ++c) std::memcpy(row + col[1 + c], &h[c], 8);
+                std::memcpy(row + col[6], &bc1, 8);
+                std::memcpy(row + col[7], &bc2, 8);
+            }
             PyObject* v = PyLong_FromLongLong(step_[k]);
             if (!v) throw py::error_already_set();
             const int rc = PyDict_SetItem(states_[k].ptr(), key_step_, v);
@@ -204,7 +212,8 @@ class PlanCore {
     std::vector<int64_t> numel_;
     std::vector<at::ScalarType> dtype_;
     std::vector<py::object> states_;
-    std::vector<std::array<py::object, 3>> srefs_;
+    std::vector<py::object> skeys_;
+    std::vector<std::vector<py::object>> srefs_;
     std::vector<uint64_t> gptr_;
     std::vector<long long> step_;
     std::vector<std::array<double, 5>> hyper_;
@@ -216,16 +225,13 @@ PYBIND11_MODULE(_gefen_host, m) {
     m.doc() = "Host-side checks of the cached Gefen step plan";
     key_params_ = intern("params");
     key_step_ = intern("step");
-    key_m_codebook_ = intern("m_codebook");
-    key_m_magnitude_ = intern("m_magnitude");
-    key_vmean_ = intern("vmean");
     key_lr_ = intern("lr");
     key_beta1_ = intern("beta1");
     key_beta2_ = intern("beta2");
     key_eps_ = intern("eps");
     key_wd_ = intern("weight_decay");
     py::class_<PlanCore>(m, "PlanCore")
-        .def(py::init<py::list, py::list, py::list>())
+        .def(py::init<py::list, py::list, py::tuple>())
         .def("refresh", &PlanCore::refresh)
         .def("__len__", &PlanCore::size);
 }

@@ -256,6 +256,10 @@ def _local(tensor):
     return tensor
 
 
+# state entries a cached plan requires to stay the same objects
+_GEFEN_STATE_KEYS = ("m_codebook", "m_magnitude", "vmean")
+
+
 class _StepPlan:
     """Cached task table of Gefen._step_all.
 
@@ -268,7 +272,8 @@ class _StepPlan:
     (and changes nothing) when the plan no longer applies.
     """
 
-    __slots__ = ("params", "pptr", "numel", "gdtype", "states", "srefs", "groups", "tasks", "device", "dev_index",
+    __slots__ = ("params", "pptr", "numel", "gdtype", "states", "state_keys", "srefs", "groups", "tasks", "device",
+                 "dev_index",
                  "grads", "gptr", "distinct", "group_index", "hyper", "core", "steps", "columns")
 
     def __init__(self, opt, items, tasks, device):
@@ -277,7 +282,8 @@ class _StepPlan:
         self.numel = [it[3].numel() for it in items]
         self.gdtype = [it[3].dtype for it in items]
         self.states = [opt.state[it[1]] for it in items]
-        self.srefs = [(st["m_codebook"], st["m_magnitude"], st["vmean"]) for st in self.states]
+        self.state_keys = _GEFEN_STATE_KEYS
+        self.srefs = [tuple(st[k] for k in self.state_keys) for st in self.states]
         self.groups = [it[0] for it in items]
         # position of each tensor's group among the distinct groups (hyperparameters are per group)
         self.distinct = _distinct(self.groups)
@@ -289,7 +295,7 @@ class _StepPlan:
         self.grads = [None] * len(items)
         self.gptr = [0] * len(items)
         self.hyper = None  # per-group hyperparameters last written into the table
-        self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.srefs)
+        self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.state_keys)
         self.steps = np.zeros(len(items), dtype=np.int64)
         fields = self.tasks.dtype.fields
         self.columns = tuple(fields[c][1] for c in ("grad", "lr", "beta1", "beta2", "eps", "weight_decay",
@@ -304,9 +310,10 @@ class _StepPlan:
                                      self.steps.ctypes.data):
                 return None
             return t
-        steps = self._refresh_python(opt)
+        steps = _plan_checks_python(self, opt)
         if steps is None:
             return None
+        t["grad"] = self.gptr
         # hyperparameters once per distinct group (the table's columns are rewritten
         # only when they change), bias corrections once per (group, step)
         hyper = []
@@ -340,46 +347,49 @@ class _StepPlan:
             t["bias_correction_2"] = bc2
         return t
 
-    def _refresh_python(self, opt):
-        """The checks of PlanCore.refresh in Python (used when the host extension
-        is not built): returns the advanced step counts, or None."""
-        params, pptr, numel, gdtype, grads, gptr = self.params, self.pptr, self.numel, self.gdtype, self.grads, self.gptr
-        n = len(params)
-        dev = self.dev_index
-        k = 0
-        for group in opt.param_groups:
-            for p in group["params"]:
-                g = p.grad
-                if g is None:
-                    continue
-                if k == n or p is not params[k]:
+
+def _plan_checks_python(plan, opt):
+    """The checks of PlanCore.refresh (gefen_amd/csrc/host_plan.cpp) in Python, for
+    a plan with params, pptr, numel, gdtype, grads, gptr, states, state_keys,
+    srefs and dev_index (used when the host extension is not built): fills plan.gptr and
+    returns the advanced step counts, or None (changing nothing) when the plan no
+    longer applies."""
+    params, pptr, numel, gdtype, grads, gptr = plan.params, plan.pptr, plan.numel, plan.gdtype, plan.grads, plan.gptr
+    n = len(params)
+    dev = plan.dev_index
+    k = 0
+    for group in opt.param_groups:
+        for p in group["params"]:
+            g = p.grad
+            if g is None:
+                continue
+            if k == n or p is not params[k]:
+                return None
+            if g is not grads[k]:
+                if (type(g) is not torch.Tensor or g.dtype is not gdtype[k] or g.numel() != numel[k]
+                        or not g.is_contiguous() or g.get_device() != dev):
                     return None
-                if g is not grads[k]:
-                    if (type(g) is not torch.Tensor or g.dtype is not gdtype[k] or g.numel() != numel[k]
-                            or not g.is_contiguous() or g.get_device() != dev):
-                        return None
-                    grads[k] = g
-                elif g.numel() != numel[k] or not g.is_contiguous():  # resized or restrided in place
-                    return None
-                if p.data_ptr() != pptr[k] or not p.is_contiguous():
-                    return None
-                gptr[k] = g.data_ptr()
-                k += 1
-        if k != n:
+                grads[k] = g
+            elif g.numel() != numel[k] or not g.is_contiguous():  # resized or restrided in place
+                return None
+            if p.data_ptr() != pptr[k] or not p.is_contiguous():
+                return None
+            gptr[k] = g.data_ptr()
+            k += 1
+    if k != n:
+        return None
+    keys = plan.state_keys
+    for st, refs in zip(plan.states, plan.srefs):
+        if any(st.get(k) is not r for k, r in zip(keys, refs)):
             return None
-        for st, (mc, mm, vm) in zip(self.states, self.srefs):
-            if st.get("m_codebook") is not mc or st.get("m_magnitude") is not mm or st.get("vmean") is not vm:
-                return None
-            if type(st.get("step")) is not int:
-                return None
-        steps = []
-        for st in self.states:
-            step = st["step"] + 1
-            st["step"] = step
-            steps.append(step)
-        self.tasks["grad"] = gptr
-        return steps
-        return t
+        if type(st.get("step")) is not int:
+            return None
+    steps = []
+    for st in plan.states:
+        step = st["step"] + 1
+        st["step"] = step
+        steps.append(step)
+    return steps
 
 
 def _distinct(objs):

@@ -18,7 +18,8 @@ import torch
 import torch.nn as nn
 
 from gefen_amd import _lib
-from gefen_amd.gefen import Gefen, _DTYPE_CODE, automatic_partition_view
+from gefen_amd.gefen import (Gefen, _DTYPE_CODE, _distinct, _gefen_host, _plan_checks_python,
+                             automatic_partition_view)
 
 EPS = 1e-7
 DEFAULT_A = 3.4445
@@ -118,6 +119,19 @@ class GefenMuon(Gefen):
             self._print_period(group["name"], local_p, period)
 
     def _step_all(self) -> None:
+        """Quantised momentum, Newton-Schulz and the parameter update of every
+        tensor.  While the same parameters carry gradients of the same layout and
+        the state tensors and Newton-Schulz settings are unchanged, a cached plan
+        (_MuonPlan) reuses the task tables and stacked buffers and only refreshes
+        gradient addresses, step counts and hyperparameters."""
+        plan = self._plan
+        if plan is not None and plan.refresh(self):
+            plan.run(self)
+            return
+        self._plan = None
+        self._step_all_build()
+
+    def _step_all_build(self) -> None:
         items = []
         for group in self.param_groups:
             for p in group["params"]:
@@ -200,6 +214,7 @@ class GefenMuon(Gefen):
                                       torch.cuda.current_stream(dev).cuda_stream)
         _lib.check(rc, "gefen_muon_tasks")
         updates = {}
+        works = {}
         if stacks:
             from gefen_amd.newton_schulz import newton_schulz_batched
 
@@ -207,7 +222,8 @@ class GefenMuon(Gefen):
                 coeffs, steps, eps = key[3], key[4], key[5]
                 _check_ns_args(coeffs, steps)
                 x = bufs[key] if key[2] == torch.bfloat16 else bufs[key].bfloat16()
-                res = newton_schulz_batched(x, coeffs, steps, eps)
+                works[key] = {}
+                res = newton_schulz_batched(x, coeffs, steps, eps, work=works[key])
                 for slot, i in enumerate(idx):
                     updates[i] = res[slot]
         apply = np.zeros(len(items), dtype=_lib.MUON_APPLY_TASK)
@@ -246,6 +262,11 @@ class GefenMuon(Gefen):
         _lib.check(rc, "gefen_muon_apply_tasks")
         for local_p, target in copy_back:
             local_p.copy_(target)
+        plain = (not copy_back and len(where) == len(items)
+                 and all(local_p is p and grad is p.grad and grad.is_contiguous() for (_, p, local_p, grad) in items))
+        if plain:
+            self._plan = _MuonPlan(self, items, tasks, apply, [(key, idx, bufs[key], works[key])
+                                                                 for key, idx in stacks.items()], dev)
         del keep
 
     @torch.no_grad()
@@ -260,3 +281,92 @@ class GefenMuon(Gefen):
         self._step_all()
         self._gefen_global_step += 1
         return loss
+
+
+class _MuonPlan:
+    """Cached task tables of GefenMuon._step_all (the GefenMuon counterpart of
+    gefen._StepPlan): the momentum and update task tables, the stacked Newton-
+    Schulz buffers and their work buffers.  ``refresh`` applies while every
+    parameter with a gradient is the recorded one with a gradient of the recorded
+    layout, the state tensors are the same objects and each group's Newton-Schulz
+    settings (coefficients, steps, eps, lr adjustment) are unchanged; it then
+    refreshes gradient addresses, step counts, lr, weight decay, momentum and
+    Nesterov, and returns True.  Otherwise it changes nothing and returns False."""
+
+    def __init__(self, opt, items, mtasks, apply, stacks, device):
+        self.params = [it[1] for it in items]
+        self.pptr = [it[1].data_ptr() for it in items]
+        self.numel = [it[3].numel() for it in items]
+        self.gdtype = [it[3].dtype for it in items]
+        self.states = [opt.state[it[1]] for it in items]
+        self.state_keys = ("m_codebook", "m_magnitude")
+        self.srefs = [tuple(st[k] for k in self.state_keys) for st in self.states]
+        self.grads = [None] * len(items)
+        self.gptr = [0] * len(items)
+        self.device = device
+        self.dev_index = device.index if device.index is not None else torch.cuda.current_device()
+        groups = [it[0] for it in items]
+        self.distinct = _distinct(groups)
+        self.group_index = np.array([next(i for i, d in enumerate(self.distinct) if d is g) for g in groups])
+        self.shapes = [tuple(it[1].shape) for it in items]
+        self.mtasks = mtasks.copy()
+        self.apply = apply.copy()
+        self.stacks = stacks
+        self.settings = self._settings()
+        self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.state_keys)
+        self.steps = np.zeros(len(items), dtype=np.int64)
+        self.mcols = (self.mtasks.dtype.fields["grad"][1],)
+
+    def _settings(self):
+        """Per distinct group: (lr, weight_decay, momentum, nesterov) and the
+        Newton-Schulz settings that shape the plan."""
+        out = []
+        for g in self.distinct:
+            lr = g["lr"]
+            out.append(((float(lr.item()) if torch.is_tensor(lr) else float(lr), g["weight_decay"], g["momentum"],
+                         bool(g["nesterov"])),
+                        (tuple(g["ns_coefficients"]), g["ns_steps"], g["eps"], g["adjust_lr_fn"])))
+        return out
+
+    def refresh(self, opt) -> bool:
+        settings = self._settings()
+        if any(a[1] != b[1] for a, b in zip(settings, self.settings)):
+            return False
+        if self.core is not None:
+            if not self.core.refresh(opt.param_groups, self.mtasks.ctypes.data, self.mtasks.itemsize, self.mcols,
+                                     self.steps.ctypes.data):
+                return False
+        else:
+            if _plan_checks_python(self, opt) is None:
+                return False
+            self.mtasks["grad"] = self.gptr
+        if settings != self.settings:
+            gi = self.group_index
+            hyper = [s[0] for s in settings]
+            lr = np.array([h[0] for h in hyper])[gi]
+            self.apply["lr"] = lr
+            self.apply["weight_decay"] = np.array([h[1] for h in hyper])[gi]
+            self.apply["adjusted_lr"] = [_adjust_lr(float(v), self.distinct[g]["adjust_lr_fn"], shape)
+                                         for v, g, shape in zip(lr, gi, self.shapes)]
+            self.mtasks["momentum"] = np.array([h[2] for h in hyper])[gi]
+            self.mtasks["nesterov"] = np.array([1 if h[3] else 0 for h in hyper])[gi]
+            self.settings = settings
+        return True
+
+    def run(self, opt) -> None:
+        from gefen_amd.newton_schulz import newton_schulz_batched
+
+        lib = _lib.load()
+        tables = opt._codebook_tables()
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            _lib.check(lib.gefen_muon_tasks(self.mtasks.ctypes.data, len(self.mtasks), tables.data_ptr(), stream),
+                       "gefen_muon_tasks")
+            for key, idx, buf, work in self.stacks:
+                coeffs, steps, eps = key[3], key[4], key[5]
+                x = buf if key[2] == torch.bfloat16 else buf.bfloat16()
+                res = newton_schulz_batched(x, coeffs, steps, eps, work=work)
+                slot_bytes = res[0].numel() * res.element_size()
+                self.apply["update"][idx] = res.data_ptr() + np.arange(len(idx), dtype=np.uint64) * slot_bytes
+            _lib.check(lib.gefen_muon_apply_tasks(self.apply.ctypes.data, len(self.apply), stream),
+                       "gefen_muon_apply_tasks")

@@ -12,7 +12,7 @@ is the one-matrix path for shapes the batched GEMM does not tile.
 
 from __future__ import annotations
 
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 
@@ -93,24 +93,37 @@ def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: 
 
 
 def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], steps: int,
-                          eps: float) -> torch.Tensor:
+                          eps: float, work: Optional[dict] = None) -> torch.Tensor:
     """Newton-Schulz of every matrix of a [G, rows, cols] bf16 stack, in place of
-    x's values (x is normalised in place); returns the [G, rows, cols] result."""
+    x's values (x is normalised in place); returns the [G, rows, cols] result.
+
+    work: a dict that keeps the intermediate buffers between calls with the same
+    stack (allocated on first use); the result is then the same buffer on every
+    call with the same number of steps."""
     a, b, c = coeffs
     g, rows, cols = x.shape
     transposed = rows > cols
+    if work is None:
+        work = {}
+
+    def buf(name, shape):
+        t = work.get(name)
+        if t is None or tuple(t.shape) != tuple(shape) or t.device != x.device:
+            t = work[name] = torch.empty(shape, dtype=torch.bfloat16, device=x.device)
+        return t
+
     # normalise each matrix, x /= max(||x||, eps) in bf16 (gefen_muon.py:37), and
     # write its transpose: X [G, m, n] with m <= n and X^T
-    other = torch.empty(g, cols, rows, dtype=torch.bfloat16, device=x.device)
+    other = buf("other", (g, cols, rows))
     lib = _lib.load()
     with torch.cuda.device(x.device):
         _lib.check(lib.gefen_ns_prepare(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps),
                                         torch.cuda.current_stream(x.device).cuda_stream), "gefen_ns_prepare")
     x, xt = (other, x) if transposed else (x, other)
     m, n = x.shape[1], x.shape[2]
-    gram = torch.empty(g, m, m, dtype=torch.bfloat16, device=x.device)
-    upd = torch.empty_like(gram)
-    nx, nxt = torch.empty_like(x), torch.empty_like(xt)
+    gram = buf("gram", (g, m, m))
+    upd = buf("upd", (g, m, m))
+    nx, nxt = buf("nx", (g, m, n)), buf("nxt", (g, n, m))
     with torch.cuda.device(x.device):
         for _ in range(steps):
             gemm_nt_batched(x, x, gram, symmetric=True)                                # X X^T

@@ -152,8 +152,7 @@ def test_plan_core_checks_and_commits_only_when_the_plan_applies():
         p.grad = torch.ones_like(p)
     states = [{"step": 3, "m_codebook": torch.zeros(1), "m_magnitude": torch.zeros(1), "vmean": torch.zeros(1)}
               for _ in ps]
-    srefs = [(st["m_codebook"], st["m_magnitude"], st["vmean"]) for st in states]
-    core = _gefen_host.PlanCore(list(ps), states, srefs)
+    core = _gefen_host.PlanCore(list(ps), states, ("m_codebook", "m_magnitude", "vmean"))
     assert len(core) == 3
     groups = [{"params": [ps[0], ps[1]], "lr": 1e-3, "beta1": 0.9, "beta2": 0.999, "eps": 1e-8, "weight_decay": 0},
               {"params": [ps[2]], "lr": torch.tensor(2e-3, dtype=torch.float64), "beta1": 0.8, "beta2": 0.99,

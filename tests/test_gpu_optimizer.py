@@ -215,3 +215,63 @@ def test_cached_step_plan_matches_rebuilt_task_table(host_checks, monkeypatch):
                                               err_msg="step {} {} {}".format(step, key, i))
             assert oa.state[pa[i]]["step"] == ob.state[pb[i]]["step"]
     assert planned >= 6  # the plan served most steps
+
+
+@pytest.mark.parametrize("host_checks", ["c++", "python"])
+def test_cached_muon_plan_matches_rebuilt_tables(host_checks, monkeypatch):
+    """GefenMuon steps through the cached plan equal steps that rebuild every table
+    and buffer, bit for bit, across an lr change, a momentum change, a Nesterov
+    switch, a skipped gradient, load_state_dict, a weight-decay change and a
+    Newton-Schulz steps change; stacks of two shapes, one of them transposed."""
+    from gefen_amd import gefen_muon as muon_mod
+    from gefen_amd.gefen_muon import GefenMuon
+
+    if host_checks == "c++":
+        assert muon_mod._gefen_host is not None, "host extension not built"
+    else:
+        monkeypatch.setattr(muon_mod, "_gefen_host", None)
+    shapes = [(256, 512), (256, 512), (512, 256), (256, 256)]
+
+    def make():
+        gen = torch.Generator().manual_seed(3)
+        return [(torch.randn(s, generator=gen) * 0.02).to(torch.bfloat16).to("cuda:0").requires_grad_(True)
+                for s in shapes]
+
+    pa, pb = make(), make()
+    oa = GefenMuon([("t{}".format(i), t) for i, t in enumerate(pa)], lr=0.02, weight_decay=0.01)
+    ob = GefenMuon([("t{}".format(i), t) for i, t in enumerate(pb)], lr=0.02, weight_decay=0.01)
+    gen = torch.Generator().manual_seed(4)
+    planned = 0
+    for step in range(1, 15):
+        for o in (oa, ob):
+            if step == 4:
+                o.param_groups[0]["lr"] = 0.01
+            if step == 6:
+                o.param_groups[1]["momentum"] = 0.9
+            if step == 8:
+                o.param_groups[2]["nesterov"] = False
+            if step == 11:
+                o.param_groups[3]["weight_decay"] = 0.1
+            if step == 13:
+                o.param_groups[0]["ns_steps"] = 4
+        if step == 10:
+            oa.load_state_dict(copy.deepcopy(oa.state_dict()))
+            ob.load_state_dict(copy.deepcopy(ob.state_dict()))
+        for i, s in enumerate(shapes):
+            g = (torch.randn(s, generator=gen) * 1e-3).to(torch.bfloat16).to("cuda:0")
+            if step == 7 and i == 1:
+                g = None
+            pa[i].grad = g
+            pb[i].grad = None if g is None else g.clone()
+        planned += oa._plan is not None
+        ob._plan = None
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for i in range(len(shapes)):
+            np.testing.assert_array_equal(gu.to_np(pa[i]), gu.to_np(pb[i]), err_msg="step {} p{}".format(step, i))
+            for key in ("m_codebook", "m_magnitude"):
+                np.testing.assert_array_equal(gu.to_np(oa.state[pa[i]][key]), gu.to_np(ob.state[pb[i]][key]),
+                                              err_msg="step {} {} {}".format(step, key, i))
+            assert oa.state[pa[i]]["step"] == ob.state[pb[i]]["step"]
+    assert planned >= 7  # the plan served most steps
