@@ -125,10 +125,18 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
     upd = buf("upd", (g, m, m))
     nx, nxt = buf("nx", (g, m, n)), buf("nxt", (g, n, m))
     with torch.cuda.device(x.device):
-        for _ in range(steps):
+        for it in range(steps):
             gemm_nt_batched(x, x, gram, symmetric=True)                                # X X^T
             gemm_nt_batched(gram, gram, upd, d_t=gram, alpha=c, beta=b, symmetric=True)  # b A + c A A
-            gemm_nt_batched(upd, xt, nx, out_t=nxt, d_t=xt, alpha=1.0, beta=a)           # a X + B X
-            x, nx = nx, x
-            xt, nxt = nxt, xt
+            if it + 1 < steps:
+                gemm_nt_batched(upd, xt, nx, out_t=nxt, d_t=xt, alpha=1.0, beta=a)       # a X + B X (and ^T)
+                x, nx = nx, x
+                xt, nxt = nxt, xt
+            elif transposed:
+                # last step, result wanted as X^T: a X^T + X^T B with B symmetric
+                gemm_nt_batched(xt, upd, nxt, d_t=x, alpha=1.0, beta=a)
+                xt = nxt
+            else:
+                gemm_nt_batched(upd, xt, nx, d_t=xt, alpha=1.0, beta=a)
+                x = nx
     return xt if transposed else x
