@@ -65,13 +65,41 @@ __global__ __launch_bounds__(256) void k_block_sums(const T* __restrict__ src, i
     }
 }
 
-// partial[b] = sum over its slice of |S[j+1]/p - S[j]/p|, j < nblocks - 1
-__global__ __launch_bounds__(256) void k_adjacent_partials(const double* __restrict__ S, int64_t nblocks, double p,
-                                                           double* __restrict__ partial) {
+// partial[b] = sum over its slice of |S[j+1]/p - S[j]/p|, j < nblocks - 1, for
+// every divisor of a batch: divisor t owns workgroups [wg_begin[t], wg_begin[t+1])
+// (one per partial), so all divisors of a gradient take one launch.
+constexpr int kAdjBatch = 80;
+struct AdjBatch {
+    int64_t s_off[kAdjBatch];    // element offset of the divisor's block sums in S
+    int64_t nblocks[kAdjBatch];
+    int64_t p_off[kAdjBatch];    // offset of the divisor's first partial
+    double p[kAdjBatch];
+    int32_t wg_begin[kAdjBatch + 1];
+    int32_t count;
+};
+static_assert(sizeof(AdjBatch) <= 4000, "kernel arguments are limited to 4 KB");
+
+__global__ __launch_bounds__(256) void k_adjacent_partials(const double* __restrict__ S0, const AdjBatch B,
+                                                           double* __restrict__ partial0) {
     __shared__ double red[4];
-    const int64_t ndiff = nblocks - 1;
-    const int64_t per = (ndiff + gridDim.x - 1) / gridDim.x;
-    const int64_t lo = (int64_t)blockIdx.x * per;
+    int t = 0;
+    {
+        int lo_t = 0, hi_t = B.count - 1;
+        while (lo_t < hi_t) {
+            const int mid = (lo_t + hi_t + 1) >> 1;
+            if (B.wg_begin[mid] <= (int)blockIdx.x) lo_t = mid;
+            else hi_t = mid - 1;
+        }
+        t = lo_t;
+    }
+    const double* __restrict__ S = S0 + B.s_off[t];
+    double* __restrict__ partial = partial0 + B.p_off[t];
+    const double p = B.p[t];
+    const int nwg = B.wg_begin[t + 1] - B.wg_begin[t];
+    const int wb = (int)blockIdx.x - B.wg_begin[t];
+    const int64_t ndiff = B.nblocks[t] - 1;
+    const int64_t per = (ndiff + nwg - 1) / nwg;
+    const int64_t lo = (int64_t)wb * per;
     const int64_t hi = lo + per < ndiff ? lo + per : ndiff;
     double s = 0.0;
     for (int64_t j = lo + threadIdx.x; j < hi; j += 256) {
@@ -81,7 +109,7 @@ __global__ __launch_bounds__(256) void k_adjacent_partials(const double* __restr
     for (int off = 32; off > 0; off >>= 1) s = s + __shfl_xor(s, off, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+    if (threadIdx.x == 0) partial[wb] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // score[d] = (sum of partials of divisor d in order) / (nblocks_d - 1); score[ndiv] = invalid count
@@ -250,8 +278,25 @@ int run_scores(const void* values, int dtype, int64_t n, const int64_t* divs, in
         }
         rc = launch_status("gefen period block sums");
         if (rc) return rc;
-        hipLaunchKernelGGL(k_adjacent_partials, dim3(P.pcount[d]), dim3(256), 0, st, S, nb, (double)p,
-                           reinterpret_cast<double*>(ws + P.off_partial) + P.pbegin[d]);
+    }
+    // the adjacent-difference partials of every divisor, kAdjBatch divisors per launch
+    for (int first = 0; first < ndiv; first += kAdjBatch) {
+        AdjBatch B;
+        memset(&B, 0, sizeof(B));
+        B.count = ndiv - first < kAdjBatch ? ndiv - first : kAdjBatch;
+        int32_t wg = 0;
+        for (int i = 0; i < B.count; ++i) {
+            const int d = first + i;
+            B.s_off[i] = P.off[d] / (int64_t)sizeof(double);
+            B.nblocks[i] = n / divs[d];
+            B.p_off[i] = P.pbegin[d];
+            B.p[i] = (double)divs[d];
+            B.wg_begin[i] = wg;
+            wg += P.pcount[d];
+        }
+        B.wg_begin[B.count] = wg;
+        hipLaunchKernelGGL(k_adjacent_partials, dim3(wg), dim3(256), 0, st, reinterpret_cast<const double*>(ws), B,
+                           reinterpret_cast<double*>(ws + P.off_partial));
         rc = launch_status("gefen period partials");
         if (rc) return rc;
     }

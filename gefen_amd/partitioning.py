@@ -7,6 +7,7 @@ follows partitioning.py:277-347 step by step.
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import List, Optional, Sequence, Tuple
 
@@ -19,6 +20,29 @@ class ZeroBlockMeanError(ValueError):
     pass
 
 
+@functools.lru_cache(maxsize=4096)
+def _all_divisors(n: int) -> Tuple[int, ...]:
+    """Every divisor of n > 0, ascending, from its prime factorisation (trial
+    division stops at the square root of what is left, so the highly composite
+    sizes of model tensors factor in a few steps)."""
+    factors = []
+    m, d = n, 2
+    while d * d <= m:
+        if m % d == 0:
+            e = 0
+            while m % d == 0:
+                m //= d
+                e += 1
+            factors.append((d, e))
+        d += 1 if d == 2 else 2
+    if m > 1:
+        factors.append((m, 1))
+    divs = [1]
+    for prime, e in factors:
+        divs = [x * prime ** k for x in divs for k in range(e + 1)]
+    return tuple(sorted(divs))
+
+
 def divisors(n, max_divisor=None) -> List[int]:
     """Divisors of n in ascending order, n itself included for n > 1
     (partitioning.py:13-30); only those <= max_divisor when it is given."""
@@ -26,17 +50,13 @@ def divisors(n, max_divisor=None) -> List[int]:
         max_divisor = int(max_divisor)
         if max_divisor < 1:
             raise ValueError("max_divisor must be positive, got {}.".format(max_divisor))
-    low, high = [], []
-    i = 1
-    while i * i <= n:
-        if n % i == 0:
-            j = n // i
-            if i != n and (max_divisor is None or i <= max_divisor):
-                low.append(i)
-            if j != i and (max_divisor is None or j <= max_divisor):
-                high.append(j)
-        i += 1
-    return low + high[::-1]
+    n = int(n)
+    if n <= 1:
+        return []
+    found = _all_divisors(n)
+    if max_divisor is None:
+        return list(found)
+    return [d for d in found if d <= max_divisor]
 
 
 def candidate_divisors(n: int, max_period: Optional[int] = None, min_num_blocks: int = DMNB) -> List[int]:
