@@ -1,5 +1,5 @@
-"""Build libgefen_hip.so (the C-ABI library), libgefen_synth.so and the host
-extension _gefen_host in-tree.
+"""Build libgefen_hip.so (the C-ABI library), libgefen_synth.so, the host
+extension _gefen_host and the GPU tests' HIP helpers (tests/hip) in-tree.
 
     python -m gefen_amd.build [--jobs N]
 
@@ -76,6 +76,21 @@ def build(jobs: int = 8, only=None) -> None:
         os.replace(tmp, out)
     if not only or "_gefen_host" in only:
         build_host_ext()
+    if not only or "test_helpers" in only:
+        build_test_helpers()
+
+
+def build_test_helpers() -> None:
+    """HIP helpers that only the GPU tests load (tests/hip/*.hip -> lib*.so beside them)."""
+    for src in sorted((REPO / "tests" / "hip").glob("*.hip")):
+        out = src.with_name("lib" + src.stem + ".so")
+        tmp = out.with_name(out.name + ".tmp")
+        cmd = [HIPCC] + COMMON + ["-shared", str(src), "-o", str(tmp)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError("hipcc failed on {}".format(src.name))
+        os.replace(tmp, out)
 
 
 def build_host_ext() -> None:
@@ -108,4 +123,4 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=8)
     args = ap.parse_args()
     build(args.jobs)
-    print("built", ", ".join(list(LIBS) + ["_gefen_host"]))
+    print("built", ", ".join(list(LIBS) + ["_gefen_host", "test helpers"]))

@@ -117,19 +117,31 @@ static_assert(offsetof(CodebookTables, thr) == 1024 && offsetof(CodebookTables, 
                   offsetof(LdsTables, cbd) == 322 * 16,
               "table layout");
 
+// Period-one stepsize of a bf16 state from a 384-entry square-root table
+// (kRootTab floats, 96 16-byte pieces; layout at root_h), optionally
+// loaded with the codebook tables (root != nullptr).
+constexpr int kRootTab = 384;
+
 template <typename D, int NT>
-__device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* T, int& K) {
+__device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* T, int& K,
+                                            const float* root = nullptr, float* root_lds = nullptr) {
     using U4 = RawVec<16>::type;
     constexpr int kPieces = 386, kPer = (kPieces + NT - 1) / NT;
+    constexpr int kRootPieces = kRootTab * 4 / 16;
+    static_assert(NT >= kRootPieces, "one root-table piece per thread");
     K = T->K;
     const U4* src = reinterpret_cast<const U4*>(T);
     U4* dst = reinterpret_cast<U4*>(&L);
     U4 v[kPer];
+    U4 rv;
+    const bool has_root = root != nullptr && threadIdx.x < kRootPieces;
+    if (has_root) rv = reinterpret_cast<const U4*>(root)[threadIdx.x];
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
         const int q = threadIdx.x + r * NT;
         if (q < kPieces) v[r] = src[q < 322 ? q + 64 : q - 322];
     }
+    if (has_root) reinterpret_cast<U4*>(root_lds)[threadIdx.x] = rv;
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
         const int q = threadIdx.x + r * NT;
@@ -166,6 +178,7 @@ __device__ __forceinline__ float stepsize_of(float v, const StepTask& T) {
 // ---------------------------------------------------------------------------
 // Gefen step, register path.  QROUND: the dequantised update cb[idx]*mag is
 // rounded to D (param dtype == state dtype) or kept in fp32 (fp32 state).
+// f16: a 32768-entry table in global memory indexed by the bits.
 template <typename S>
 __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
     if constexpr (sizeof(S) == 2) {
@@ -173,6 +186,39 @@ __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
         if (GEFEN_STEP_P1_LUT && T.lut && !(bits & 0x8000u)) return T.lut[bits];
     }
     return stepsize_of(to_f32(v), T);
+}
+
+// Period-one stepsize of a bf16 state value (bits) from the LDS square-root
+// table root.  A finite v >= 0 is M * 2^E with an integer M < 256 (128 +
+// mantissa for normal v, the mantissa for subnormal v), E = max(exponent
+// field, 1) - 134.  With par = E mod 2 and half = floor(E / 2) = (bits >> 8) - 67,
+// sqrt(v) = sqrt(M * 2^par) * 2^half, and since every value here is a normal
+// float (sqrt(v) >= 2^-67, sqrt(bc2) >= 2^-27), scaling by powers of two
+// commutes with rounding:
+//   fl(fl(sqrt(v)) / sqrt_bc2) = root[i] * 2^(bits >> 8)   exactly, with
+//   i = bits & 0xff   for normal v (= par * 128 + mantissa; E and the exponent
+//                     field have the same parity),
+//   i = 256 + bits    for subnormal v and zero (par = 1),
+//   root[i] = fl(fl(sqrt(M * 2^par)) / sqrt_bc2) * 2^-67   (k_build_root).
+// root_h returns h = that + eps.
+__device__ __forceinline__ float root_h(uint32_t bits, const StepTask& T, const float* root) {
+    const uint32_t i = bits < 0x80u ? bits + 256u : (bits & 0xffu);
+    return __builtin_ldexpf(root[i], (int)(bits >> 8)) + T.eps;
+}
+
+// root_h and the reciprocal are exact where this holds: v finite and >= 0
+// (bits < 0x7f80) and 2^-126 <= h < 2^126.  In that range the reciprocal
+// fma(fma(-h, r, 1), r, r) with r = v_rcp_f32(h) equals the IEEE quotient 1 / h
+// (checked on gfx950 for every float h in the range); other values take
+// stepsize_of.
+__device__ __forceinline__ bool root_ok(uint32_t bits, float h) {
+    return bits < 0x7f80u && __float_as_uint(h) - 0x00800000u < 0x7e000000u;
+}
+
+__device__ __forceinline__ float root_stepsize(float h, const StepTask& T) {
+    const float r = __builtin_amdgcn_rcpf(h);
+    const float e = __builtin_fmaf(-h, r, 1.0f);
+    return __builtin_fmaf(e, r, r) * T.inv_bc1;
 }
 
 // Nearest index with at most two threshold probes (max_probe <= 2): one
@@ -193,7 +239,7 @@ __device__ __forceinline__ int nearest_two_probe(float x, const float* thr, cons
 // (gefen.py:1280-1281) is applied to the parameter first.
 template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST, bool WD, typename UF>
 __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
-                                            const UF& upd_of, const Vec<D, W> (&gv)[R],
+                                            const float* root, const UF& upd_of, const Vec<D, W> (&gv)[R],
                                             const Vec<D, W> (&pv)[R], const Vec<S, W> (&vv)[R], uint8_t* idx, D* p,
                                             S* vm, uint32_t base, int lir, int lpr, bool active, int K, float mn,
                                             double rb, float ss) {
@@ -203,6 +249,37 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
         Vec<uint8_t, W> io;
         Vec<D, W> po;
         Vec<S, W> vo;
+        float sw[W];  // period one: stepsize of each element's new vmean
+        if constexpr (P1) {
+            bool special = false;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float gf = to_f32(gv[j].v[w]);
+                const float sq = gf * gf;  // mean over a one-element row
+                const float prev = to_f32(vv[j].v[w]) * T.b2;
+                const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
+                vo.v[w] = vnew;
+                if constexpr (std::is_same<S, bf16_t>::value) {
+                    if (root) {
+                        const float h = root_h(vnew.bits, T, root);
+                        special = special || !root_ok(vnew.bits, h);
+                        sw[w] = root_stepsize(h, T);
+                    } else {
+                        sw[w] = stepsize_of(to_f32(vnew), T);
+                    }
+                } else {
+                    sw[w] = p1_stepsize<S>(vnew, T);
+                }
+            }
+            if constexpr (std::is_same<S, bf16_t>::value) {
+                if (special) {  // one branch per vector for the rare values outside the table's range
+#pragma unroll
+                    for (int w = 0; w < W; ++w)
+                        if (!root_ok(vo.v[w].bits, root_h(vo.v[w].bits, T, root)))
+                            sw[w] = stepsize_of(to_f32(vo.v[w]), T);
+                }
+            }
+        }
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             int k;
@@ -221,15 +298,7 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
             } else {
                 float q = L.cbd[k] * mn;
                 if (QROUND) q = round_to<D>(q);
-                float s = ss;
-                if (P1) {
-                    const float gf = to_f32(gv[j].v[w]);
-                    const float sq = gf * gf;  // mean over a one-element row
-                    const float prev = to_f32(vv[j].v[w]) * T.b2;
-                    const S vnew = from_f32<S>(__builtin_fmaf(sq, T.omb2, prev));
-                    vo.v[w] = vnew;
-                    s = p1_stepsize<S>(vnew, T);
-                }
+                const float s = P1 ? sw[w] : ss;
                 u = (q * s) * T.lr;
             }
             float pf = to_f32(pv[j].v[w]);
@@ -257,10 +326,15 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
 // idempotent under such copies; the sum of squares masks them out.
 template <typename D, typename S, int W, int R, bool P1, bool TAB>
 __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) {
+    constexpr bool kRoot = P1 && std::is_same<S, bf16_t>::value;
     __shared__ LdsTables L;
     __shared__ float row_tab[TAB ? kStepWaves : 1][TAB ? 2 : 1][2][256];
+    __shared__ __attribute__((aligned(16))) float root_lds[kRoot ? kRootTab : 4];
+    // every task of a launch has the same stepsize table (flush_steps)
+    const float* root_src = kRoot ? B.t[0].lut : nullptr;
+    const float* root = root_src ? root_lds : nullptr;  // uniform
     int K;
-    load_tables<D, kStepThreads>(L, B.tables, K);
+    load_tables<D, kStepThreads>(L, B.tables, K, root_src, root_lds);
     const bool two_probe = B.tables->max_probe <= 2;
     const int ti = find_task(B.wg_begin, B.ntasks);
     const StepTask T = B.t[ti];
@@ -387,7 +461,7 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
 #define GEFEN_SWEEP2(FAST, WD)                                                                                 \
-    step_sweep2<D, S, W, R, P1, TAB, FAST, WD>(T, L, utab, upd_of, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K, \
+    step_sweep2<D, S, W, R, P1, TAB, FAST, WD>(T, L, utab, root, upd_of, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K, \
                                                mn, rb, ss)
         if (T.do_wd) {
             if (fast) GEFEN_SWEEP2(true, true);
@@ -852,7 +926,19 @@ __global__ __launch_bounds__(kThreads) void k_muon_packed(const MuonBatch B) {
 }
 
 // ---------------------------------------------------------------------------
-// Stepsize table of a period-one tensor with a 16-bit state: lut[b] is the
+// The bf16 square-root table of root_h: root[i] = fl(fl(sqrt(M * 2^par)) /
+// sqrt_bc2) * 2^-67 with (par, M) = (i >> 7, 128 + (i & 127)) for i < 256 and
+// (1, i - 256) for 256 <= i < 384.
+__global__ __launch_bounds__(256) void k_build_root(float* __restrict__ root, StepTask T) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < kRootTab) {
+        const int par = i < 256 ? (i >> 7) : 1;
+        const int m = i < 256 ? 128 + (i & 127) : i - 256;
+        root[i] = __builtin_ldexpf(sqrtf((float)m * (par ? 2.0f : 1.0f)) / T.sqrt_bc2, -67);
+    }
+}
+
+// Stepsize table of a period-one tensor with an f16 state: lut[b] is the
 // stepsize (gefen.py:1326-1327) of the non-negative state value with bits b,
 // computed by the same expression as the per-block path, so lookups are exact.
 template <typename S>
@@ -1081,6 +1167,8 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
         int64_t wg = 0;
         for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
             if (done[j] || !(pend[j].key == pend[i].key)) continue;
+            // one stepsize table per launch: workgroups load it before they find their task
+            if (pend[j].task.lut != pend[i].task.lut) continue;
             if (wg + pend[j].task.nwg > kMaxLaunchWgs) break;
             b.t[n] = pend[j].task;
             b.wg_begin[n] = (int32_t)wg;
@@ -1113,7 +1201,10 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     const int dsz = dtype_size(in.param_dtype), ssz = dtype_size(in.state_dtype);
     const int W = pick_width(dsz, rowlen, {in.p, in.grad}, 1, in.m_codebook, ssz, p1 ? in.vmean : nullptr);
     const int64_t nvec = rowlen / W;
-    const int l2 = lpr_log2_for(nvec);
+    // period-one rows (at most 256 * 64 elements) take half the lanes with
+    // twice the vectors per lane: more bytes in flight per lane
+    int l2 = lpr_log2_for(nvec);
+    if (p1 && l2 > 0) --l2;
     int R = r_bucket(nvec, l2);
     if (p1 && R == 0) return fail_inval("period_one_divisor %lld is too large", (long long)rowlen);
     // row tables pay off when a row has at least as many elements as codewords per lane group
@@ -1149,8 +1240,9 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
 }
 
 // Build the stepsize tables of the period-one tasks with a 16-bit state (one
-// table per distinct (dtype, sqrt(bc2), eps, 1/bc1)); *buf owns them until the
-// launches that read them are enqueued.
+// table per distinct (dtype, sqrt(bc2), eps, 1/bc1): the 384-entry square-root
+// table for bf16, the 32768-entry stepsize table for f16); *buf owns them until
+// the launches that read them are enqueued.
 int prepare_luts(std::vector<PendingStep>& pend, hipStream_t st, void** buf) {
     struct LutKey { int s; float a, b, c; };
     std::vector<LutKey> keys;
@@ -1182,7 +1274,7 @@ int prepare_luts(std::vector<PendingStep>& pend, hipStream_t st, void** buf) {
         t.eps = keys[j].b;
         t.inv_bc1 = keys[j].c;
         if (keys[j].s == GEFEN_BF16)
-            hipLaunchKernelGGL(k_build_lut<bf16_t>, dim3(128), dim3(256), 0, st, base + j * 32768, t);
+            hipLaunchKernelGGL(k_build_root, dim3((kRootTab + 255) / 256), dim3(256), 0, st, base + j * 32768, t);
         else
             hipLaunchKernelGGL(k_build_lut<f16_t>, dim3(128), dim3(256), 0, st, base + j * 32768, t);
         int rc = launch_status("gefen stepsize table");

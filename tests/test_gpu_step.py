@@ -67,7 +67,26 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_step_tasks_match_oracle(case):
-    name, dt, sdt, n, period, wd = case
+    _run_case(*case)
+
+
+# Period-one bf16 states over the whole bf16 range: per-row gradient scales from
+# 2^-66 to 2^18 put the new vmean on subnormals, zero, every exponent in between
+# and large values, each read through the kernel's square-root table.
+WIDE_CASES = [
+    ("bf16_P1_wide_b2_half", 256 * 96, 0.5, 1e-8, -66, 18),
+    ("bf16_P1_wide_eps_small", 256 * 96, 0.999, 1e-12, -66, 18),
+    ("bf16_P1_wide_eps_large", 64 * 75, 0.9, 1e-3, -40, 10),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_CASES, ids=[c[0] for c in WIDE_CASES])
+def test_period_one_bf16_stepsize_over_the_value_range(case):
+    name, n, b2, eps, e_lo, e_hi = case
+    _run_case(name, "bf16", "bf16", n, 1, 0.0, e_lo=e_lo, e_hi=e_hi, b2=b2, eps=eps)
+
+
+def _run_case(name, dt, sdt, n, period, wd, e_lo=-14, e_hi=-4, b2=0.999, eps=1e-8):
     print("case", name, flush=True)
     cb = _codebook()
     seed = sum(map(ord, name))
@@ -85,10 +104,10 @@ def test_step_tasks_match_oracle(case):
     cb_dev = torch.from_numpy(cb).to("cuda:0")
     tables = _tables(cb_dev)
     lib = _lib.load()
-    b1, b2, lr, eps = 0.9, 0.999, 1e-3, 1e-8
+    b1, lr = 0.9, 1e-3
     for step in range(1, 5):
         grows = n // period if period > 1 else (n // 64 if n % 64 == 0 else 1)
-        g = syn.round_to(syn.row_scaled_normal(seed, step, grows, n // grows, -14, -4), dt).reshape(-1)
+        g = syn.round_to(syn.row_scaled_normal(seed, step, grows, n // grows, e_lo, e_hi), dt).reshape(-1)
         g = g.view(np.uint16) if g.dtype == np.float16 else g
         g_dev = gu.to_dev(g, dt)
         bc1, bc2 = 1 - b1 ** step, 1 - b2 ** step
