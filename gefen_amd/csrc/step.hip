@@ -1462,7 +1462,10 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     const int dsz = dtype_size(in.grad_dtype);
     const int W = pick_width(dsz, rowlen, {in.grad, in.out}, 1, in.m_codebook, 0, nullptr);
     const int64_t nvec = rowlen / W;
-    const int l2 = lpr_log2_for(nvec);
+    // rows of at most 32 vectors take half the lanes with twice the vectors per
+    // lane (measured 6% faster on the Qwen3-1.7B momentum, mostly period-one rows)
+    int l2 = lpr_log2_for(nvec);
+    if (l2 > 0 && l2 <= 5) --l2;
     const int R = r_bucket(nvec, l2);
     // row tables pay off for whole-wave rows (measured: 5% faster there, none for 32-lane rows)
     const int tab = (R != 0 && l2 >= GEFEN_MUON_TAB_LOG2) ? 1 : 0;
