@@ -16,6 +16,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1155,14 +1156,55 @@ struct PendingStep {
     StepTask task;
 };
 
+// A second stream per device (default priority) for the small launches of a
+// step, forked from and joined back to the caller's stream with events, so the
+// launches of small tensors run beside the large ones instead of after them.
+struct SideStream {
+    std::mutex m;
+    bool tried = false;
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxDevices = 64;
+SideStream g_side[kMaxDevices];
+
+// Launches of fewer elements than this go to the side stream.
+constexpr int64_t kSmallLaunchElems = 1 << 20;
+
+SideStream* side_stream() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    SideStream& ss = g_side[dev];
+    std::lock_guard<std::mutex> lock(ss.m);
+    if (!ss.tried) {
+        ss.tried = true;
+        if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) {
+            ss.s = nullptr;
+            (void)hipGetLastError();
+        }
+    }
+    return ss.s ? &ss : nullptr;
+}
+
 int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st) {
-    // group by kernel key, launch up to kMaxBatch tasks per launch
+    // group by kernel key, up to kMaxBatch tasks per launch
+    struct Launch {
+        Key key;
+        StepBatch b;
+        int wg;
+        int64_t elems;
+    };
+    std::vector<Launch> launches;
     std::vector<bool> done(pend.size(), false);
     for (size_t i = 0; i < pend.size(); ++i) {
         if (done[i]) continue;
-        StepBatch b;
-        memset(&b, 0, sizeof(b));
-        b.tables = tables;
+        Launch L;
+        memset(&L.b, 0, sizeof(L.b));
+        L.key = pend[i].key;
+        L.b.tables = tables;
+        L.elems = 0;
         int n = 0;
         int64_t wg = 0;
         for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
@@ -1170,17 +1212,35 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
             // one stepsize table per launch: workgroups load it before they find their task
             if (pend[j].task.lut != pend[i].task.lut) continue;
             if (wg + pend[j].task.nwg > kMaxLaunchWgs) break;
-            b.t[n] = pend[j].task;
-            b.wg_begin[n] = (int32_t)wg;
+            L.b.t[n] = pend[j].task;
+            L.b.wg_begin[n] = (int32_t)wg;
             wg += pend[j].task.nwg;
+            L.elems += pend[j].task.nrows * pend[j].task.rowlen;
             ++n;
             done[j] = true;
         }
-        b.wg_begin[n] = (int32_t)wg;
-        b.ntasks = n;
-        if (wg == 0) continue;
-        hipError_t e = dispatch_step(pend[i].key, b, (int)wg, st);
+        L.b.wg_begin[n] = (int32_t)wg;
+        L.b.ntasks = n;
+        L.wg = (int)wg;
+        if (wg > 0) launches.push_back(L);
+    }
+    bool any_small = false, any_large = false;
+    for (const Launch& L : launches) (L.elems < kSmallLaunchElems ? any_small : any_large) = true;
+    SideStream* side = (any_small && any_large) ? side_stream() : nullptr;
+    std::unique_lock<std::mutex> lock;
+    if (side) {
+        lock = std::unique_lock<std::mutex>(side->m);
+        if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
+            return launch_status("gefen step fork");
+    }
+    for (const Launch& L : launches) {
+        hipStream_t ls = (side && L.elems < kSmallLaunchElems) ? side->s : st;
+        hipError_t e = dispatch_step(L.key, L.b, L.wg, ls);
         if (e != hipSuccess) return hip_status(e, "gefen step launch");
+    }
+    if (side) {
+        if (hipEventRecord(side->join, side->s) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
+            return launch_status("gefen step join");
     }
     return GEFEN_OK;
 }
