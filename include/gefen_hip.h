@@ -128,7 +128,7 @@ typedef struct gefen_step_task {
 /* All tasks of one call, batched into a few launches.  Launches of small
  * tensors may run on a library-owned second stream of the device, forked from
  * `stream` and joined back to it with events: the work is still ordered on
- * `stream` (and capturable), but tasks of one call must not share memory. */
+ * `stream`, but tasks of one call must not share memory. */
 int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const void* tables,
                      gefen_stream_t stream);
 
