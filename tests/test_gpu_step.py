@@ -249,6 +249,7 @@ def test_many_tasks_in_one_call():
         rows_m = n // (pod if period == 1 else period)
         p = syn.round_to(syn.normal(syn.make_key(11, i), n) * 0.02, dt)
         g = syn.round_to(syn.row_scaled_normal(11, 1000 + i, max(1, n // 64), 64, -14, -4), dt).reshape(-1)
+        assert g.size == n
         d = {"p": gu.to_dev(p, dt), "g": gu.to_dev(g, dt), "idx": torch.zeros(n, dtype=torch.uint8, device="cuda:0"),
              "mag": torch.zeros(rows_m, dtype=gu.TORCH[dt], device="cuda:0"),
              "v": torch.zeros(n // period, dtype=gu.TORCH[dt], device="cuda:0")}
@@ -272,6 +273,60 @@ def test_many_tasks_in_one_call():
     for d, o in zip(devs, oracle):
         np.testing.assert_array_equal(gu.to_np(d["idx"]), o["idx"])
         np.testing.assert_array_equal(gu.to_np(d["mag"]), o["mag"])
+
+
+def test_small_launches_on_the_side_stream_match_the_oracle():
+    """A call mixing large launches (at least 2^20 elements) with small ones: the
+    small launches run on the library's second stream, forked from and joined back
+    to the caller's stream.  Every tensor matches the oracle, including period-one
+    tensors on both streams (each reading the shared stepsize table) and a read of
+    the results right after the call on the caller's stream."""
+    cb = _codebook()
+    cb_dev = torch.from_numpy(cb).to("cuda:0")
+    tables = _tables(cb_dev)
+    specs = [("bf16", 2048 * 600, 2048), ("bf16", 256 * 4200, 1), ("bf16", 256 * 12, 1), ("bf16", 768 * 5, 768),
+             ("f32", 96 * 8, 96), ("bf16", 2304, 18), ("f32", 1024 * 1100, 1024)]
+    tasks = np.zeros(len(specs), dtype=_lib.STEP_TASK)
+    devs, oracle = [], []
+    for i, (dt, n, period) in enumerate(specs):
+        pod = orc.largest_divisor_at_most(n, 256) if period == 1 else 0
+        rows_m = n // (pod if period == 1 else period)
+        p = syn.round_to(syn.normal(syn.make_key(21, i), n) * 0.02, dt)
+        g = syn.round_to(syn.row_scaled_normal(21, 500 + i, n // 64, 64, -14, -4), dt).reshape(-1)
+        assert g.size == n and p.size == n
+        d = {"p": gu.to_dev(p, dt), "g": gu.to_dev(g, dt), "idx": torch.zeros(n, dtype=torch.uint8, device="cuda:0"),
+             "mag": torch.zeros(rows_m, dtype=gu.TORCH[dt], device="cuda:0"),
+             "v": torch.zeros(n // period, dtype=gu.TORCH[dt], device="cuda:0")}
+        devs.append(d)
+        oracle.append({"p": p.copy(), "g": g, "idx": np.zeros(n, np.uint8), "mag": np.zeros(rows_m, orc.NP_STORAGE[dt]),
+                       "v": np.zeros(n // period, orc.NP_STORAGE[dt]), "dt": dt, "n": n, "period": period, "pod": pod})
+        t = tasks[i]
+        t["p"], t["grad"], t["m_codebook"] = d["p"].data_ptr(), d["g"].data_ptr(), d["idx"].data_ptr()
+        t["m_magnitude"], t["vmean"] = d["mag"].data_ptr(), d["v"].data_ptr()
+        t["numel"], t["period"], t["period_one_divisor"] = n, period, pod
+        t["param_dtype"] = t["state_dtype"] = gu.CODE[dt]
+        t["beta1"], t["beta2"], t["lr"], t["eps"] = 0.9, 0.999, 1e-3, 1e-8
+        t["bias_correction_1"], t["bias_correction_2"] = 0.1, 1 - 0.999
+    _lib.check(_lib.load().gefen_step_tasks(tasks.ctypes.data, len(specs), tables.data_ptr(), gu.stream()))
+    # read on the caller's stream without a device-wide synchronisation first
+    got = [{k: d[k].clone() for k in ("p", "idx", "mag", "v")} for d in devs]
+    for o in oracle:
+        orc.lib().orc_gefen_step(gu.CODE[o["dt"]], gu.CODE[o["dt"]], orc._ptr(o["p"]), orc._ptr(o["g"]),
+                                 orc._ptr(o["idx"]), orc._ptr(o["mag"]), orc._ptr(o["v"]), o["n"], o["period"],
+                                 o["pod"], orc._ptr(cb), 256, 0.9, 0.999, 1e-3, 1e-8, 0.0, 0.1, 1 - 0.999, 1)
+    torch.cuda.synchronize()
+    for (dt, n, period), d, o in zip(specs, got, oracle):
+        print("side stream case", dt, n, period, flush=True)
+        np.testing.assert_array_equal(gu.to_np(d["idx"]), o["idx"])
+        np.testing.assert_array_equal(gu.to_np(d["mag"]), o["mag"])
+        pg = gu.to_np(d["p"])
+        if period == 1:
+            np.testing.assert_array_equal(gu.to_np(d["v"]), o["v"])
+            np.testing.assert_array_equal(pg, o["p"])
+        elif dt == "f32":
+            np.testing.assert_allclose(pg, o["p"], rtol=1e-5, atol=1e-7)
+        else:
+            assert _ulps(pg, o["p"]).max() <= 1
 
 
 def test_invalid_arguments_raise_value_error():
