@@ -14,7 +14,9 @@ log-uniform scale in [2^-17, 2^-7] (~[1e-5, 1e-2]).
 * roofline: algorithmic HBM bytes of one step (p read+write, g read, 8-bit
   index read+write, per-block state read+write with the chosen periods) divided
   by the GPU time of the fused step kernels, measured with HIP events on the
-  launch stream around ``gefen_step_tasks``.
+  launch stream around ``gefen_step_tasks``.  copy_kernel_gbs: a plain 2 GiB
+  device copy (16-byte vectors) timed the same way on the same box, and
+  frac_of_copy the step kernels' bandwidth as a fraction of it.
 * cpu_baseline: the CPU oracle (C restatement of the reference CPU path,
   OpenMP) on a bounded sample of the same tensors, scaled to a full step.
 """
@@ -297,6 +299,28 @@ def muon_ns_roofline(opt, params, reps=3):
             "note": "Newton-Schulz of every stack of one step, normalisation included"}
 
 
+def copy_ceiling_gbs(dev, nbytes=1 << 31, reps=5):
+    """HBM bandwidth of a plain 16-byte-vector copy kernel on this box (bytes read +
+    written per second, HIP events on the launch stream): the ceiling the step
+    kernels' streaming traffic is also compared against."""
+    from gefen_amd import synthetic as syn
+
+    src = torch.ones(nbytes // 2, dtype=torch.int16, device=dev)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    syn.copy_device(src, dst)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        syn.copy_device(src, dst)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2.0 * nbytes / (ms * 1e-3) / 1e9
+
+
 def cpu_baseline(opt, params, budget_s=20.0):
     """Oracle (reference CPU path restated in C, OpenMP over blocks) on a sample
     of the tensors, scaled by bytes to one full step."""
@@ -426,9 +450,11 @@ def main():
         kms = e0.elapsed_time(e1) / reps
         nbytes = step_bytes(opt, params)
         achieved = nbytes / (kms * 1e-3) / 1e9
+        copy_gbs = copy_ceiling_gbs(dev)
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg, nbytes),
-                           "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes)}
+                           "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes),
+                           "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline(opt, params)
     else:
