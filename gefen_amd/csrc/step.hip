@@ -1171,9 +1171,18 @@ SideStream g_side[kMaxDevices];
 // Launches of fewer elements than this go to the side stream.
 constexpr int64_t kSmallLaunchElems = 1 << 20;
 
-SideStream* side_stream() {
+// The side stream of the current device, or nullptr (then everything runs on
+// st): also when st belongs to another device than the current one.
+SideStream* side_stream(hipStream_t st) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    if (st) {
+        hipDevice_t sdev = -1;
+        if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
     SideStream& ss = g_side[dev];
     std::lock_guard<std::mutex> lock(ss.m);
     if (!ss.tried) {
@@ -1226,7 +1235,7 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
     }
     bool any_small = false, any_large = false;
     for (const Launch& L : launches) (L.elems < kSmallLaunchElems ? any_small : any_large) = true;
-    SideStream* side = (any_small && any_large) ? side_stream() : nullptr;
+    SideStream* side = (any_small && any_large) ? side_stream(st) : nullptr;
     std::unique_lock<std::mutex> lock;
     if (side) {
         lock = std::unique_lock<std::mutex>(side->m);
