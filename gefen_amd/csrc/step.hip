@@ -177,9 +177,10 @@ __device__ __forceinline__ float stepsize_of(float v, const StepTask& T) {
 }
 
 // ---------------------------------------------------------------------------
-// Gefen step, register path.  QROUND: the dequantised update cb[idx]*mag is
-// rounded to D (param dtype == state dtype) or kept in fp32 (fp32 state).
-// f16: a 32768-entry table in global memory indexed by the bits.
+// Gefen step, register path.
+
+// Period-one stepsize of an f16 state value from the 32768-entry table in
+// global memory indexed by its bits (k_build_lut); fp32 states compute it.
 template <typename S>
 __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
     if constexpr (sizeof(S) == 2) {
@@ -233,11 +234,14 @@ __device__ __forceinline__ int nearest_two_probe(float x, const float* thr, cons
     return k;
 }
 
-// Second sweep of a row: quantise, dequantise, update p.  FAST: the block
-// magnitude is finite and positive and the two-probe search is exact.  Every
-// lane computes all R vectors (out-of-row vectors hold a copy of the row's last
-// vector); only in-row vectors of active rows are stored.  WD: weight decay
-// (gefen.py:1280-1281) is applied to the parameter first.
+// Second sweep of a row: quantise, dequantise, update p.  QROUND: the
+// dequantised update cb[idx]*mag is rounded to D (param dtype == state dtype)
+// or kept in fp32 (fp32 state).  FAST: the block magnitude is finite and
+// positive and the two-probe search is exact.  Every lane computes all R
+// vectors (out-of-row vectors hold a copy of the row's last vector); only
+// in-row vectors of active rows are stored.  WD: weight decay
+// (gefen.py:1280-1281) is applied to the parameter first.  root: the LDS
+// square-root table of a period-one bf16 state, or nullptr.
 template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST, bool WD, typename UF>
 __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
                                             const float* root, const UF& upd_of, const Vec<D, W> (&gv)[R],
