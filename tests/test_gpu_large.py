@@ -1,7 +1,8 @@
-"""Tensors past 2^31 elements.  Every output of the step depends only on its own
-magnitude block, the codebook and scalars, so the last blocks of a tensor of
-more than 2^31 elements, stepped inside it, must equal the same blocks stepped
-as a tensor of their own -- bit for bit, through two steps."""
+"""Full sizes, through block locality.  Every output of the step depends only on
+its own magnitude block, the codebook and scalars, so the last blocks of a tensor
+of more than 2^31 elements, stepped inside it, must equal the same blocks stepped
+as a tensor of their own -- bit for bit, through two steps -- and every tensor of
+the full 8B-shaped step must equal itself stepped alone."""
 
 import numpy as np
 import pytest
@@ -64,3 +65,56 @@ def test_blocks_past_2_31_elements_match_a_tensor_of_their_own(period):
     assert torch.equal(mag[-(tail // blk):].view(torch.int16), mags.view(torch.int16))
     assert torch.equal(vm[-(tail // period):].view(torch.int16), vms.view(torch.int16))
     assert int(idxs.to(torch.int32).sum()) > 0  # the step did quantise something
+
+
+def test_full_8b_step_equals_its_tensors_stepped_alone():
+    """The Llama-3-8B-shaped step of bench.py at full size (291 tensors, 8.03e9
+    bf16 elements, the optimizer's own periods and learned codebook) through the
+    optimizer's batched, multi-launch, two-stream path: sampled tensors (the
+    embedding, block-row and period-one projections, norms) must equal the same
+    tensors stepped one at a time from a snapshot -- bit for bit."""
+    import bench
+    from gefen_amd.gefen import Gefen
+
+    dev = torch.device("cuda:0")
+    params = bench.build_problem(bench.CONFIGS["llama8b"], dev)
+    print("8B problem built", flush=True)
+    opt = Gefen(params)
+    opt.step()  # periods, codebook, states
+    torch.cuda.synchronize()
+    sample = [0, 1, 2, 3, 4, 5, 6, 7, 8, 150, len(params) - 2, len(params) - 1]
+    snap = []
+    for i in sample:
+        _, p = params[i]
+        st = opt.state[p]
+        snap.append({"p": p.detach().clone(), "idx": st["m_codebook"].clone(), "mag": st["m_magnitude"].clone(),
+                     "v": st["vmean"].clone(), "period": st["automatic_period"],
+                     "pod": st.get("period_one_divisor", 0), "step": st["step"]})
+    opt.step()  # every tensor in one call of the step kernels
+    tables = opt._codebook_tables()
+    lib = _lib.load()
+    kinds = set()
+    for i, s in zip(sample, snap):
+        _, p = params[i]
+        st = opt.state[p]
+        g = opt.param_groups[i]
+        step = s["step"] + 1
+        t = np.zeros(1, dtype=_lib.STEP_TASK)
+        t["p"], t["grad"], t["m_codebook"] = s["p"].data_ptr(), p.grad.data_ptr(), s["idx"].data_ptr()
+        t["m_magnitude"], t["vmean"] = s["mag"].data_ptr(), s["v"].data_ptr()
+        t["numel"], t["period"] = p.numel(), s["period"]
+        t["period_one_divisor"] = s["pod"] if s["period"] == 1 else 0
+        t["param_dtype"] = t["state_dtype"] = gu.CODE["bf16"]
+        t["beta1"], t["beta2"], t["lr"], t["eps"], t["weight_decay"] = (g["beta1"], g["beta2"], g["lr"], g["eps"],
+                                                                         g["weight_decay"])
+        t["bias_correction_1"] = 1 - g["beta1"] ** step
+        t["bias_correction_2"] = 1 - g["beta2"] ** step
+        _lib.check(lib.gefen_step_tasks(t.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+        torch.cuda.synchronize()
+        print("tensor", i, params[i][0], p.numel(), "period", s["period"], flush=True)
+        kinds.add("one" if s["period"] == 1 else ("small" if p.numel() < 2 ** 20 else "rows"))
+        assert torch.equal(p.detach().view(torch.int16), s["p"].view(torch.int16))
+        assert torch.equal(st["m_codebook"], s["idx"])
+        assert torch.equal(st["m_magnitude"].view(torch.int16), s["mag"].view(torch.int16))
+        assert torch.equal(st["vmean"].view(torch.int16), s["v"].view(torch.int16))
+    assert kinds == {"one", "small", "rows"}, kinds
