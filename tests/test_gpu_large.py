@@ -118,3 +118,52 @@ def test_full_8b_step_equals_its_tensors_stepped_alone():
         assert torch.equal(st["m_magnitude"].view(torch.int16), s["mag"].view(torch.int16))
         assert torch.equal(st["vmean"].view(torch.int16), s["v"].view(torch.int16))
     assert kinds == {"one", "small", "rows"}, kinds
+
+
+def test_full_qwen3_muon_momentum_equals_its_tensors_stepped_alone():
+    """GefenMuon at bench.py's full Qwen3-1.7B shapes (196 matrices, cached plan,
+    stacked Newton-Schulz): the quantised momentum state of sampled matrices after
+    a step equals gefen_muon_tasks run on each of them alone from a snapshot, bit
+    for bit."""
+    import bench
+    from gefen_amd.gefen import _DTYPE_CODE
+    from gefen_amd.gefen_muon import GefenMuon
+
+    dev = torch.device("cuda:0")
+    params = bench.build_problem(bench.CONFIGS["muon"], dev)
+    print("Qwen3 problem built", flush=True)
+    opt = GefenMuon(params)
+    opt.step()
+    opt.step()  # the second step builds the cached plan
+    torch.cuda.synchronize()
+    sample = [0, 1, 2, 3, 4, 5, 6, len(params) - 1]
+    snap = []
+    for i in sample:
+        _, p = params[i]
+        st = opt.state[p]
+        snap.append({"idx": st["m_codebook"].clone(), "mag": st["m_magnitude"].clone(),
+                     "period": st["automatic_period"]})
+    opt.step()  # through the cached plan
+    tables = opt._codebook_tables()
+    lib = _lib.load()
+    periods = set()
+    for i, s in zip(sample, snap):
+        _, p = params[i]
+        st = opt.state[p]
+        g = opt.param_groups[i]
+        flat = p.grad.reshape(-1)
+        out = torch.empty_like(flat)
+        t = np.zeros(1, dtype=_lib.MUON_TASK)
+        t["grad"], t["m_codebook"], t["m_magnitude"], t["out"] = (flat.data_ptr(), s["idx"].data_ptr(),
+                                                                   s["mag"].data_ptr(), out.data_ptr())
+        t["numel"] = flat.numel()
+        t["block"] = opt._period_one_divisor_from_state(st, flat.numel()) if s["period"] == 1 else s["period"]
+        t["grad_dtype"], t["state_dtype"] = _DTYPE_CODE[flat.dtype], _DTYPE_CODE[st["m_magnitude"].dtype]
+        t["momentum"], t["nesterov"] = g["momentum"], 1 if g["nesterov"] else 0
+        _lib.check(lib.gefen_muon_tasks(t.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+        torch.cuda.synchronize()
+        print("matrix", i, params[i][0], tuple(p.shape), "period", s["period"], flush=True)
+        periods.add(s["period"] == 1)
+        assert torch.equal(st["m_codebook"], s["idx"])
+        assert torch.equal(st["m_magnitude"].view(torch.int16), s["mag"].view(torch.int16))
+    assert periods == {True, False}, periods
