@@ -284,11 +284,26 @@ __global__ void k_dp_backtrack(int K, int force, int bins, char* __restrict__ ws
 }
 
 // ---------------------------------------------------------------------------
-// Lloyd-Max accumulators (reference CUDA semantics; fp32 sums are order dependent)
+// Lloyd-Max accumulators (reference CUDA semantics; fp32 sums are order dependent).
+// The block absmax skips NaN elements as the reference's running maximum does
+// (lloyd_max_fused_kernel.cu:78-95, 141-158).
 struct LloydLds {
     float thr[260];
     uint16_t bucket[4100];
 };
+
+// Codeword of a normalised value in the Lloyd kernels, as the reference's
+// binary search picks it (lloyd_max_fused_kernel.cu:17-48): the lower bound k
+// and its left neighbour k-1, ties to the left.  For x inside the codebook this
+// is nearest_index.  It differs in two places: NaN (no codeword compares below
+// it, and NaN distances fail the <= test) takes index 0, and x above the last
+// codeword compares the last two entries instead of taking the last one.
+__device__ __forceinline__ int lloyd_index(float x, const float* thr, const uint16_t* bucket, int K, float cb_prev,
+                                           float cb_last) {
+    if (x != x) return 0;
+    if (K >= 2 && x > cb_last) return fabsf(x - cb_prev) <= fabsf(x - cb_last) ? K - 2 : K - 1;
+    return nearest_index(x, thr, bucket, K);
+}
 
 template <typename G>
 __global__ __launch_bounds__(256) void k_lloyd_accumulate(const G* __restrict__ g, int64_t nrows, int64_t period,
@@ -299,6 +314,7 @@ __global__ __launch_bounds__(256) void k_lloyd_accumulate(const G* __restrict__ 
     __shared__ float s_sum[256];
     __shared__ uint32_t s_cnt[256];
     const int K = T->K;
+    const float cb_last = T->cb[K - 1], cb_prev = T->cb[K >= 2 ? K - 2 : 0];
     for (int i = threadIdx.x; i < 260; i += 256) L.thr[i] = T->thr[i];
     for (int i = threadIdx.x; i < 4100; i += 256) L.bucket[i] = T->bucket[i];
     s_sum[threadIdx.x] = 0.0f;
@@ -308,12 +324,12 @@ __global__ __launch_bounds__(256) void k_lloyd_accumulate(const G* __restrict__ 
     for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < nrows; row += (int64_t)gridDim.x * 4) {
         const int64_t base = row * period;
         float amax = 0.0f;
-        for (int64_t j = lane; j < period; j += 64) amax = nanmax(amax, fabsf(to_f32(g[base + j])));
-        amax = group_max(amax, 64);
+        for (int64_t j = lane; j < period; j += 64) amax = max_skip_nan(amax, fabsf(to_f32(g[base + j])));
+        amax = group_max_skip_nan(amax, 64);
         for (int64_t j = lane; j < period; j += 64) {
             const float v = to_f32(g[base + j]);
             const float x = (amax > 0.0f) ? v / amax : 0.0f;
-            const int k = nearest_index(x, L.thr, L.bucket, K);
+            const int k = lloyd_index(x, L.thr, L.bucket, K, cb_prev, cb_last);
             atomicAdd(&s_sum[k], x);
             atomicAdd(&s_cnt[k], 1u);
         }
@@ -335,6 +351,7 @@ __global__ __launch_bounds__(256) void k_lloyd_mse(const G* __restrict__ g, int6
     __shared__ LloydLds L;
     __shared__ float red[2][4];
     const int K = T->K;
+    const float cb_last = T->cb[K - 1], cb_prev = T->cb[K >= 2 ? K - 2 : 0];
     for (int i = threadIdx.x; i < 260; i += 256) L.thr[i] = T->thr[i];
     for (int i = threadIdx.x; i < 4100; i += 256) L.bucket[i] = T->bucket[i];
     __syncthreads();
@@ -343,12 +360,12 @@ __global__ __launch_bounds__(256) void k_lloyd_mse(const G* __restrict__ g, int6
     for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < nrows; row += (int64_t)gridDim.x * 4) {
         const int64_t base = row * period;
         float amax = 0.0f;
-        for (int64_t j = lane; j < period; j += 64) amax = nanmax(amax, fabsf(to_f32(g[base + j])));
-        amax = group_max(amax, 64);
+        for (int64_t j = lane; j < period; j += 64) amax = max_skip_nan(amax, fabsf(to_f32(g[base + j])));
+        amax = group_max_skip_nan(amax, 64);
         for (int64_t j = lane; j < period; j += 64) {
             const float v = to_f32(g[base + j]);
             const float x = (amax > 0.0f) ? v / amax : 0.0f;
-            const int k = nearest_index(x, L.thr, L.bucket, K);
+            const int k = lloyd_index(x, L.thr, L.bucket, K, cb_prev, cb_last);
             const float err = x - new_cb[k];
             const float e2 = err * err;
             en = en + e2;

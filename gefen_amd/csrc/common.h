@@ -63,6 +63,9 @@ __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v
 
 // NaN-propagating maximum of non-negative values (torch amax semantics)
 __device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
+// Maximum that skips NaN: b replaces a only when b > a, a comparison NaN never
+// passes (the running-maximum loops of lloyd_max_fused_kernel.cu:78-95).
+__device__ __forceinline__ float max_skip_nan(float a, float b) { return b > a ? b : a; }
 
 // ----------------------------------------------------------------- vector access
 // W consecutive elements of type T moved with one load/store of W*sizeof(T) bytes.
@@ -123,6 +126,10 @@ __device__ __forceinline__ void vstore32_nt(T* base, uint32_t elem, const Vec<T,
 // Butterfly over groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_max(float v, int width) {
     for (int off = width >> 1; off > 0; off >>= 1) v = nanmax(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float group_max_skip_nan(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v = max_skip_nan(v, __shfl_xor(v, off, 64));
     return v;
 }
 __device__ __forceinline__ float group_sum(float v, int width) {

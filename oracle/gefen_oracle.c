@@ -17,6 +17,9 @@
  *   exact DP codebook    quantization.py:68-81, 151-258 (+ gefen.py:373-399)
  *   period scores        partitioning.py:43-78, 119-167 (numpy pairwise sums)
  *   GefenMuon momentum   gefen_muon.py:132-171, 302-316
+ *   Lloyd-Max, block variance / CoV: the reference's CUDA kernels
+ *                        (lloyd_max_fused_kernel.cu:17-195,
+ *                        period_variance_kernel.cu:13-106), which have no CPU path
  *
  * Rounding conventions (verified against torch 2.10 CPU): lerp and
  * add(alpha=) are fused multiply-adds; tensor/scalar is a true division;
@@ -578,5 +581,111 @@ int orc_muon_momentum(int ddt, int sdt, const void* g, uint8_t* idx, void* mag,
 /* out[i] = fma(a[i], b, c[i]) in fp32 (torch fp32 add_(x, alpha=b) on CPU) */
 int orc_fma32(const float* a, float b, const float* c, float* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = fmaf(a[i], b, c[i]);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ Lloyd-Max
+ * The reference's CUDA semantics (lloyd_max_fused_kernel.cu:17-195; it has no
+ * CPU counterpart): per block, absmax = running maximum of |g| that a NaN never
+ * replaces (lines 78-95); x = g / absmax in float32, 0 when absmax is 0; the
+ * codeword from the binary search of lines 17-48 (first k with cb[k] >= x, its
+ * left neighbour, ties to the left; NaN takes index 0, x above the last
+ * codeword compares the last two).  The kernels add the sums and squared errors
+ * in float32 in their own order; here they are added in double. */
+static inline int lloyd_index(const float* cb, int K, float x) {
+    int left = 0, right = K;
+    while (left < right) {
+        const int mid = left + (right - left) / 2;
+        if (cb[mid] < x) left = mid + 1; else right = mid;
+    }
+    int r = left;
+    if (r < 0) r = 0; else if (r >= K) r = K - 1;
+    int l = r - 1;
+    if (l < 0) l = 0;
+    const float dl = fabsf(x - cb[l]), dr = fabsf(x - cb[r]);
+    return dl <= dr ? l : r;
+}
+
+static float lloyd_absmax(const void* g, int dt, int64_t s, int64_t len) {
+    float m = 0.0f;
+    for (int64_t j = 0; j < len; ++j) {
+        const float a = fabsf(load_dt(g, dt, s + j));
+        if (a > m) m = a;
+    }
+    return m;
+}
+
+int orc_lloyd_accumulate(int gdt, const void* g, int64_t n, int64_t period, const float* cb, int K,
+                         double* sums, int64_t* counts) {
+    if (period <= 0 || n % period || K <= 0 || K > 256) return 1;
+    for (int64_t s = 0; s < n; s += period) {
+        const float amax = lloyd_absmax(g, gdt, s, period);
+        for (int64_t j = 0; j < period; ++j) {
+            const float v = load_dt(g, gdt, s + j);
+            const float x = amax > 0.0f ? v / amax : 0.0f;
+            const int k = lloyd_index(cb, K, x);
+            sums[k] += (double)x;
+            counts[k] += 1;
+        }
+    }
+    return 0;
+}
+
+/* out[0] += sum of (x - new[k])^2, out[1] += sum of ((x - new[k]) * absmax)^2,
+ * each term formed in float32 as lines 166-175 do. */
+int orc_lloyd_mse(int gdt, const void* g, int64_t n, int64_t period, const float* old_cb, const float* new_cb,
+                  int K, double* out) {
+    if (period <= 0 || n % period || K <= 0 || K > 256) return 1;
+    for (int64_t s = 0; s < n; s += period) {
+        const float amax = lloyd_absmax(g, gdt, s, period);
+        for (int64_t j = 0; j < period; ++j) {
+            const float v = load_dt(g, gdt, s + j);
+            const float x = amax > 0.0f ? v / amax : 0.0f;
+            const int k = lloyd_index(old_cb, K, x);
+            const float err = x - new_cb[k];
+            const float e2 = err * err;
+            const float oe = err * amax;
+            const float o2 = oe * oe;
+            out[0] += (double)e2;
+            out[1] += (double)o2;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ block variance / CoV
+ * The reference's CUDA scorers (period_variance_kernel.cu:13-106, 177-318), in
+ * double: per block, x = v (input_is_squared) or v*v in float32; mean and
+ * E[x^2] over the block, var = max(E[x^2] - mean^2, 0).  variance: out[0] =
+ * sqrt(mean of var over blocks).  CoV: out[0] = sum of sqrt(var)/mean over
+ * blocks with mean > 0, out[1] = their count, out[2] = count of mean < 0. */
+int orc_block_variance(int gdt, const void* v, int64_t n, int64_t period, int input_is_squared, int cov,
+                       double* out) {
+    if (period <= 0 || n % period) return 1;
+    const int64_t nb = n / period;
+    double acc = 0.0, cnt = 0.0, neg = 0.0;
+    for (int64_t b = 0; b < nb; ++b) {
+        double sx = 0.0, sx2 = 0.0;
+        for (int64_t j = 0; j < period; ++j) {
+            const float a = load_dt(v, gdt, b * period + j);
+            const double x = input_is_squared ? (double)a : (double)(a * a);
+            sx += x;
+            sx2 += x * x;
+        }
+        const double mean = sx / (double)period;
+        double var = sx2 / (double)period - mean * mean;
+        if (var < 0.0) var = 0.0;
+        if (!cov) {
+            acc += var;
+        } else if (mean < 0.0) {
+            neg += 1.0;
+        } else if (mean > 0.0) {
+            acc += sqrt(var) / mean;
+            cnt += 1.0;
+        }
+    }
+    out[0] = cov ? acc : sqrt(acc / (double)nb);
+    out[1] = cnt;
+    out[2] = neg;
     return 0;
 }

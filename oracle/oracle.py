@@ -10,8 +10,10 @@ the reference algorithm that are integer logic or small host code:
 * ``finalize_period`` (partitioning.py:277-347) and ``find_period``
   (partitioning.py:119-167 + gefen.py:812-828);
 * ``learn_codebook`` (gefen.py:305-419: histograms, fp32 accumulation, DP);
-* ``newton_schulz`` (gefen_muon.py:16-51) in float64 with a bf16 rounding of
-  every torch op output, and ``adjust_lr`` (gefen_muon.py:54-67);
+* Newton-Schulz (gefen_muon.py:16-51) one torch op at a time (``ns_normalize``,
+  ``ns_gram``, ``ns_poly``, ``ns_update``: exact products, one bf16 rounding
+  each), ``muon_apply`` (gefen_muon.py:325-329) and ``adjust_lr``
+  (gefen_muon.py:54-67);
 * ``GefenOracle`` / ``GefenMuonOracle``: whole optimizer steps on numpy arrays,
   following ``Gefen.step`` / ``GefenMuon.step`` on the CPU path.
 
@@ -60,10 +62,14 @@ def lib():
         L.orc_gefen_update_given.argtypes = [I, I, P, P, P, P, P, I, P, I64, I64, P, I, D, D, D, D, D]
         L.orc_unpack_nibbles.argtypes = [P, I64, P]
         L.orc_pack_nibbles.argtypes = [P, I64, P]
+        L.orc_lloyd_accumulate.argtypes = [I, P, I64, I64, P, I, P, P]
+        L.orc_lloyd_mse.argtypes = [I, P, I64, I64, P, P, I, P]
+        L.orc_block_variance.argtypes = [I, P, I64, I64, I, I, P]
         for name in ("orc_gefen_step", "orc_vmean_update", "orc_nearest", "orc_histogram",
                      "orc_accumulate_counts", "orc_exact_dp", "orc_period_scores",
                      "orc_muon_momentum", "orc_f32_to_bf16", "orc_f32_to_f16", "orc_fma32",
-                     "orc_gefen_update_given", "orc_unpack_nibbles", "orc_pack_nibbles"):
+                     "orc_gefen_update_given", "orc_unpack_nibbles", "orc_pack_nibbles",
+                     "orc_lloyd_accumulate", "orc_lloyd_mse", "orc_block_variance"):
             getattr(L, name).restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -221,25 +227,86 @@ def nearest(cb: np.ndarray, x: np.ndarray) -> np.ndarray:
 
 
 # ----------------------------------------------------------------- Newton-Schulz
-def newton_schulz_bf16(u_f32: np.ndarray, coeffs=(3.4445, -4.7750, 2.0315), steps: int = 5,
-                       eps: float = 1e-7) -> np.ndarray:
-    """gefen_muon.py:16-51 with float64 products and a bf16 rounding after every
-    torch op (input cast, norm, clamp, div_, each matmul / addmm)."""
-    a, b, c = coeffs
-    x = round_f32(u_f32.astype(np.float32), "bf16").astype(np.float64)
-    transposed = u_f32.shape[0] > u_f32.shape[1]
-    if transposed:
-        x = x.T.copy()
+# Each torch op of gefen_muon.py:16-51 on bf16 tensors, as a bf16 rounding of
+# the exact result: the products are formed in float64 (exact for these sizes up
+# to the final rounding), rounded to float32 and then to bf16.  torch-CPU sums
+# its bf16 products in float32, so its result differs from this one only where
+# the float32 accumulation error reaches a bf16 rounding boundary: within one
+# bf16 ulp plus 2(K+1)*2^-24 * sum|terms| of every element (checked against the
+# reference's own products, tests/golden/ns_products.npz).
+
+def _bf16_of(x64: np.ndarray) -> np.ndarray:
+    return from_f32(np.asarray(x64, dtype=np.float64).astype(np.float32), "bf16")
+
+
+def _f64_of(bits: np.ndarray) -> np.ndarray:
+    return to_f32(bits, "bf16").astype(np.float64)
+
+
+def ns_normalize(g_bits: np.ndarray, eps: float = 1e-7) -> np.ndarray:
+    """gefen_muon.py:33-37: X = bf16(G), transposed when rows > cols, then
+    X.div_(X.norm().clamp(min=eps)): the norm and the clamp are bf16 tensors,
+    the quotient is rounded to bf16.  Returns X (bf16 bits, [min, max] shape)."""
+    x = _f64_of(g_bits)
+    if x.shape[0] > x.shape[1]:
+        x = x.T
     nrm = float(round_f32(np.array([np.sqrt(np.sum(x * x))], dtype=np.float32), "bf16")[0])
     nrm = float(round_f32(np.array([max(nrm, np.float32(eps))], dtype=np.float32), "bf16")[0])
-    x = round_f32((x / nrm).astype(np.float32), "bf16").astype(np.float64)
+    return _bf16_of(x / nrm)
+
+
+def ns_gram(x_bits: np.ndarray) -> np.ndarray:
+    """gefen_muon.py:39: A = X @ X.T."""
+    x = _f64_of(x_bits)
+    return _bf16_of(x @ x.T)
+
+
+def ns_poly(a_bits: np.ndarray, b: float, c: float) -> np.ndarray:
+    """gefen_muon.py:40-46: B = torch.addmm(A, A, A, beta=b, alpha=c) = b A + c A A."""
+    a = _f64_of(a_bits)
+    return _bf16_of(b * a + c * (a @ a))
+
+
+def ns_update(b_bits: np.ndarray, x_bits: np.ndarray, a: float) -> np.ndarray:
+    """gefen_muon.py:47: X' = torch.addmm(X, B, X, beta=a) = a X + B X."""
+    x = _f64_of(x_bits)
+    return _bf16_of(a * x + _f64_of(b_bits) @ x)
+
+
+def ns_term_bound(op: str, lhs_bits: np.ndarray, rhs_bits: Optional[np.ndarray] = None,
+                  a: float = 0.0, b: float = 0.0, c: float = 0.0) -> np.ndarray:
+    """2(K+1) * 2^-24 * sum|terms| of each element of a product above (float64):
+    what two float32 accumulations of the same K products may differ by."""
+    u = 2.0 ** -24
+    if op == "gram":
+        x = np.abs(_f64_of(lhs_bits))
+        return 2 * (x.shape[1] + 1) * u * (x @ x.T)
+    if op == "poly":
+        m = np.abs(_f64_of(lhs_bits))
+        return 2 * (m.shape[1] + 1) * u * (abs(b) * m + abs(c) * (m @ m))
+    bm, x = np.abs(_f64_of(lhs_bits)), np.abs(_f64_of(rhs_bits))
+    return 2 * (bm.shape[1] + 1) * u * (abs(a) * x + bm @ x)
+
+
+def ulp_bf16(bits: np.ndarray) -> np.ndarray:
+    """The bf16 ulp at each value (float64), 2^-133 for zero and subnormals."""
+    v = np.abs(_f64_of(bits))
+    e = np.floor(np.log2(np.maximum(v, 2.0 ** -126)))
+    return np.ldexp(1.0, (e - 7).astype(np.int64))
+
+
+def newton_schulz_bf16(u_f32: np.ndarray, coeffs=(3.4445, -4.7750, 2.0315), steps: int = 5,
+                       eps: float = 1e-7) -> np.ndarray:
+    """gefen_muon.py:16-51: ns_normalize, then `steps` times ns_gram, ns_poly,
+    ns_update; the result is transposed back for a tall input.  float32 values
+    of the bf16 result."""
+    a, b, c = coeffs
+    x = ns_normalize(from_f32(np.asarray(u_f32, dtype=np.float32), "bf16"), eps)
     for _ in range(steps):
-        A = round_f32((x @ x.T).astype(np.float32), "bf16").astype(np.float64)
-        B = round_f32((b * A + c * (A @ A)).astype(np.float32), "bf16").astype(np.float64)
-        x = round_f32((a * x + B @ x).astype(np.float32), "bf16").astype(np.float64)
-    if transposed:
-        x = x.T.copy()
-    return x.astype(np.float32)
+        x = ns_update(ns_poly(ns_gram(x), b, c), x, a)
+    if u_f32.shape[0] > u_f32.shape[1]:
+        x = np.ascontiguousarray(x.T)
+    return to_f32(x, "bf16")
 
 
 def adjust_lr(lr: float, adjust_lr_fn: Optional[str], shape) -> float:
@@ -360,6 +427,42 @@ def gefen_update_given(dtype: str, sdtype: str, p: np.ndarray, g: np.ndarray, id
         raise RuntimeError("orc_gefen_update_given failed: {}".format(rc))
 
 
+def lloyd_accumulate(g: np.ndarray, dtype: str, period: int, codebook: np.ndarray):
+    """Per-codeword sums (float64) and counts of the block-normalised values
+    (lloyd_max_fused_kernel.cu:50-107 semantics, see gefen_oracle.c)."""
+    g = np.ascontiguousarray(g.reshape(-1))
+    cb = np.ascontiguousarray(codebook, dtype=np.float32)
+    sums = np.zeros(cb.size, dtype=np.float64)
+    counts = np.zeros(cb.size, dtype=np.int64)
+    rc = lib().orc_lloyd_accumulate(DT[dtype], _ptr(g), g.size, period, _ptr(cb), cb.size, _ptr(sums), _ptr(counts))
+    if rc:
+        raise ValueError("orc_lloyd_accumulate: bad arguments")
+    return sums, counts
+
+
+def lloyd_mse(g: np.ndarray, dtype: str, period: int, old_codebook: np.ndarray, new_codebook: np.ndarray):
+    """(normalised, original) squared-error sums in float64 (lloyd_max_fused_kernel.cu:109-195)."""
+    g = np.ascontiguousarray(g.reshape(-1))
+    oc = np.ascontiguousarray(old_codebook, dtype=np.float32)
+    nc = np.ascontiguousarray(new_codebook, dtype=np.float32)
+    out = np.zeros(2, dtype=np.float64)
+    rc = lib().orc_lloyd_mse(DT[dtype], _ptr(g), g.size, period, _ptr(oc), _ptr(nc), oc.size, _ptr(out))
+    if rc:
+        raise ValueError("orc_lloyd_mse: bad arguments")
+    return float(out[0]), float(out[1])
+
+
+def block_variance(v: np.ndarray, dtype: str, period: int, input_is_squared: bool, cov: bool) -> np.ndarray:
+    """[sqrt(mean block variance), 0, 0] or [sum CoV, count, negative count]
+    (period_variance_kernel.cu:13-106 semantics in float64)."""
+    v = np.ascontiguousarray(v.reshape(-1))
+    out = np.zeros(3, dtype=np.float64)
+    rc = lib().orc_block_variance(DT[dtype], _ptr(v), v.size, period, int(input_is_squared), int(cov), _ptr(out))
+    if rc:
+        raise ValueError("orc_block_variance: bad arguments")
+    return out
+
+
 def unpack_nibbles(packed: np.ndarray, n: int) -> np.ndarray:
     """Packed 4-bit indices -> one byte per element (automatic_gefen_fused_kernel.cu:14-27)."""
     out = np.empty(n, dtype=np.uint8)
@@ -385,6 +488,10 @@ class GefenMuonOracle(GefenOracle):
         self.nesterov = nesterov
         self.ns = (ns_coefficients, ns_steps, eps)
         self.adjust_lr_fn = adjust_lr_fn
+        # per tensor, of its last step: the Nesterov blend (Newton-Schulz input,
+        # gradient dtype) and the Newton-Schulz result (bf16 bits)
+        self.last_blend: List[Optional[np.ndarray]] = [None] * len(params)
+        self.last_update: List[Optional[np.ndarray]] = [None] * len(params)
 
     def step(self, grads: Sequence[Optional[np.ndarray]]) -> None:
         self.refresh_codebook(grads)
@@ -399,27 +506,36 @@ class GefenMuonOracle(GefenOracle):
             u32 = to_f32(upd, dt).reshape(shape)
             coeffs, steps, eps = self.ns
             U = newton_schulz_bf16(u32, coeffs, steps, eps)
+            self.last_blend[i] = upd
+            self.last_update[i] = from_f32(U, "bf16")
             lr = prm["lr"]
-            adj = adjust_lr(lr, self.adjust_lr_fn, shape)
-            p = prm["p"]
-            pf = to_f32(p, dt).reshape(-1)
-            if prm["weight_decay"] > 0.0:
-                pf = round_f32(pf * np.float32(1 - lr * prm["weight_decay"]), dt)
-            Uf = np.ascontiguousarray(U.reshape(-1))
-            if dt == "f32":
-                # p.add_(U, alpha): promote(f32, bf16) = f32, one fused multiply-add
-                newp = _fma32(Uf, np.float32(-adj), pf)
-            else:
-                # reduced-float add_ with alpha rounded to the dtype.  The update of a
-                # tall matrix (rows > cols) is a transposed view, which takes the
-                # element-wise path where the product is rounded to the dtype too.
-                al = round_f32(np.array([-adj], dtype=np.float32), dt)[0]
-                prod = (Uf * al).astype(np.float32)
-                if shape[0] > shape[1]:
-                    prod = round_f32(prod, dt)
-                newp = round_f32((pf + prod).astype(np.float32), dt)
-            p[...] = from_f32(newp, dt).reshape(p.shape)
+            muon_apply(prm["p"], self.last_update[i], dt, shape, lr, prm["weight_decay"],
+                       adjust_lr(lr, self.adjust_lr_fn, shape))
         self.global_step += 1
+
+
+def muon_apply(p: np.ndarray, u_bits: np.ndarray, dtype: str, shape, lr: float, weight_decay: float,
+               adjusted_lr: float) -> None:
+    """gefen_muon.py:325-329 on the CPU path, p updated in place (storage dtype):
+    p.mul_(1 - lr * wd) when wd > 0, then p.add_(U, alpha=-adjusted_lr) with the
+    bf16 Newton-Schulz result U in the parameter's layout."""
+    pf = to_f32(p, dtype).reshape(-1)
+    if weight_decay > 0.0:
+        pf = round_f32(pf * np.float32(1 - lr * weight_decay), dtype)
+    Uf = np.ascontiguousarray(to_f32(u_bits, "bf16").reshape(-1))
+    if dtype == "f32":
+        # p.add_(U, alpha): promote(f32, bf16) = f32, one fused multiply-add
+        newp = _fma32(Uf, np.float32(-adjusted_lr), pf)
+    else:
+        # reduced-float add_ with alpha rounded to the dtype.  The update of a
+        # tall matrix (rows > cols) is a transposed view, which takes the
+        # element-wise path where the product is rounded to the dtype too.
+        al = round_f32(np.array([-adjusted_lr], dtype=np.float32), dtype)[0]
+        prod = (Uf * al).astype(np.float32)
+        if shape[0] > shape[1]:
+            prod = round_f32(prod, dtype)
+        newp = round_f32((pf + prod).astype(np.float32), dtype)
+    p[...] = from_f32(newp, dtype).reshape(p.shape)
 
 
 def _fma32(a: np.ndarray, b: np.float32, c: np.ndarray) -> np.ndarray:

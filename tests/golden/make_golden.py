@@ -15,7 +15,11 @@ reference is copied.  The fixtures pin what no closed form can:
   ``gefen.py:305-419``, ``quantization.py:206-258``);
 * 20-step trajectories of ``Gefen`` / ``GefenMuon`` on the CPU path
   (``gefen.py:1208-1333``, ``gefen_muon.py:216-329``);
-* the ``state_dict`` layout (``gefen.py:1343-1349``).
+* the ``state_dict`` layout (``gefen.py:1343-1349``);
+* every bf16 product of the reference's Newton-Schulz iterations
+  (``gefen_muon.py:16-51``, ``ns_products.npz``) and, along the GefenMuon
+  trajectories, each step's Newton-Schulz input and output and the parameter
+  before and after its update (``gefen_muon.py:302-329``, ``muon_steps_*.npz``).
 """
 
 from __future__ import annotations
@@ -43,10 +47,19 @@ TORCH_DTYPE = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat1
 
 
 def import_reference(path: str):
+    """Import the reference under its own package name ``gefen`` (its modules import
+    each other as ``gefen.*``).  This repository's ``gefen`` package (the import
+    surface over ``gefen_amd``) must not answer instead: the reference's directory
+    goes first on sys.path, nothing named gefen may be imported yet, and the
+    imported package must live under ``path``."""
+    if any(name == "gefen" or name.startswith("gefen.") for name in sys.modules):
+        raise RuntimeError("a module named gefen is already imported; run this script in a fresh process")
     tmp = tempfile.mkdtemp(prefix="gefen_ref_")
     os.symlink(path, os.path.join(tmp, "gefen"))
     sys.path.insert(0, tmp)
     import gefen  # noqa: F401
+    if not os.path.realpath(gefen.__file__).startswith(os.path.realpath(path)):
+        raise RuntimeError("imported {} instead of the reference at {}".format(gefen.__file__, path))
     import gefen.gefen as ref_gefen
     import gefen.gefen_muon as ref_muon
     import gefen.partitioning as ref_part
@@ -286,6 +299,136 @@ def make_traj(ref, out: Path, name: str, codebook: np.ndarray) -> None:
     print("traj", name, "periods", periods, "in", round(time.time() - t0, 1), "s", flush=True)
 
 
+# --------------------------------------------------------------------------- Newton-Schulz
+# (name, rows, cols, seed stream): the bf16 products of every iteration of
+# _zeropower_via_newtonschulz (gefen_muon.py:16-51) on seeded bf16 inputs
+NS_CASES = [
+    ("ns_256x512", 256, 512, 1),
+    ("ns_512x256", 512, 256, 2),
+    ("ns_128x384", 128, 384, 3),
+]
+NS_COEFFS = (3.4445, -4.7750, 2.0315)
+NS_STEPS = 5
+NS_EPS = 1e-7
+
+
+class _AddmmSpy:
+    """Stands in for the reference module's ``torch``: records the operands and
+    result of every torch.addmm call; every other attribute is torch's."""
+
+    def __init__(self):
+        self.calls = []
+
+    def addmm(self, inp, mat1, mat2, *, beta=1, alpha=1):
+        out = torch.addmm(inp, mat1, mat2, beta=beta, alpha=alpha)
+        self.calls.append((inp.clone(), mat1.clone(), mat2.clone(), beta, alpha, out.clone()))
+        return out
+
+    def __getattr__(self, name):
+        return getattr(torch, name)
+
+
+def make_ns(ref, out: Path) -> None:
+    """Each iteration k of the reference's Newton-Schulz on bf16 input G:
+    X_{k-1} (ortho_grad entering the iteration), A_k = X X^T (the operand of the
+    first addmm), B_k = addmm(A, A, A, beta=b, alpha=c) and X_k = addmm(X, B, X,
+    beta=a); X_0 is the normalised input, and ``out`` the function's result."""
+    _, ref_muon, _, _ = ref
+    seed = 5150
+    data = {}
+    manifest = []
+    real_torch = ref_muon.torch
+    for name, rows, cols, stream in NS_CASES:
+        g = syn.round_to(syn.normal(syn.make_key(seed, stream), rows * cols) * 1e-3, "bf16").reshape(rows, cols)
+        spy = _AddmmSpy()
+        ref_muon.torch = spy
+        try:
+            res = ref_muon._zeropower_via_newtonschulz(to_torch(g, "bf16"), NS_COEFFS, NS_STEPS, NS_EPS)
+        finally:
+            ref_muon.torch = real_torch
+        calls = spy.calls
+        assert len(calls) == 2 * NS_STEPS, len(calls)
+        data[name + "/g"] = g
+        data[name + "/x0"] = to_numpy(calls[1][2])  # mat2 of the first X update: the normalised X
+        for k in range(NS_STEPS):
+            gram_in, _, _, beta_b, alpha_c, b_out = calls[2 * k]
+            x_in, b_in, x_in2, beta_a, _, x_out = calls[2 * k + 1]
+            assert beta_b == NS_COEFFS[1] and alpha_c == NS_COEFFS[2] and beta_a == NS_COEFFS[0]
+            assert torch.equal(x_in.view(torch.int16), x_in2.view(torch.int16))
+            assert torch.equal(b_in.view(torch.int16), b_out.view(torch.int16))
+            data["{}/a{}".format(name, k + 1)] = to_numpy(gram_in)
+            data["{}/b{}".format(name, k + 1)] = to_numpy(b_out)
+            data["{}/x{}".format(name, k + 1)] = to_numpy(x_out)
+            if k > 0:
+                assert torch.equal(x_in.view(torch.int16), calls[2 * k - 1][5].view(torch.int16))
+        data[name + "/out"] = to_numpy(res)
+        manifest.append({"name": name, "shape": [rows, cols], "seed": seed, "stream": stream,
+                         "coefficients": list(NS_COEFFS), "steps": NS_STEPS, "eps": NS_EPS,
+                         "checksum_g": syn.checksum(g.reshape(-1))})
+        print("ns", name, flush=True)
+    np.savez_compressed(out / "ns_products.npz", **data)
+    (out / "ns_products.json").write_text(json.dumps(manifest, indent=1))
+
+
+# GefenMuon steps at which the Newton-Schulz input / output and the parameter
+# before / after the update are recorded (muon trajectories)
+MUON_STEP_CAPTURE = (1, 2, 10)
+
+
+def make_muon_steps(ref, out: Path, name: str, codebook: np.ndarray) -> None:
+    """Replays the GefenMuon trajectory `name` on the reference and records, at
+    MUON_STEP_CAPTURE, every tensor's Newton-Schulz input (the Nesterov blend,
+    gefen_muon.py:312-316), its output, and the parameter before and after the
+    step (gefen_muon.py:318-329)."""
+    ref_gefen, ref_muon, _, _ = ref
+    set_name, dtype, kind, steps, kwargs, (e_lo, e_hi) = TRAJ_CASES[name]
+    assert kind == "muon"
+    pset = getattr(ps, set_name)
+    seed = 2024 + sum(map(ord, name))
+    params = []
+    for i, (pname, shape, mode) in enumerate(pset):
+        t = to_torch(ps.init_param(seed, i, shape, dtype), dtype).requires_grad_(True)
+        params.append((pname, t, mode))
+    opt = ref_muon.GefenMuon([(n, t) for n, t, _ in params], **kwargs)
+    opt._gefen_codebook = torch.from_numpy(codebook.astype(np.float32)).clone()
+    real_ns = ref_muon._zeropower_via_newtonschulz
+    seen = []
+
+    def spy(grad, coeffs, ns_steps, eps):
+        # the input first: for a bf16 input, grad.bfloat16() is grad itself, which
+        # the normalisation then divides in place (gefen_muon.py:33-37)
+        ns_in = grad.detach().clone()
+        res = real_ns(grad, coeffs, ns_steps, eps)
+        seen.append((ns_in, res.detach().clone()))
+        return res
+
+    data = {}
+    last = max(MUON_STEP_CAPTURE)
+    ref_muon._zeropower_via_newtonschulz = spy
+    try:
+        for step in range(1, last + 1):
+            for i, (pname, t, mode) in enumerate(params):
+                g = ps.grad_for_step(seed, i, step, tuple(t.shape), dtype, mode, e_lo, e_hi)
+                t.grad = to_torch(g, dtype)
+            before = [to_numpy(t) for _, t, _ in params]
+            seen.clear()
+            opt.step()
+            assert len(seen) == len(params)
+            if step in MUON_STEP_CAPTURE:
+                for i, (pname, t, _) in enumerate(params):
+                    data["p{}/step{}/before".format(i, step)] = before[i]
+                    data["p{}/step{}/after".format(i, step)] = to_numpy(t)
+                    data["p{}/step{}/ns_in".format(i, step)] = to_numpy(seen[i][0])
+                    data["p{}/step{}/ns_out".format(i, step)] = to_numpy(seen[i][1])
+    finally:
+        ref_muon._zeropower_via_newtonschulz = real_ns
+    np.savez_compressed(out / "muon_steps_{}.npz".format(name), **data)
+    (out / "muon_steps_{}.json".format(name)).write_text(json.dumps(
+        {"name": name, "steps": list(MUON_STEP_CAPTURE), "ns_in_dtype": "bf16" if dtype == "bf16" else dtype,
+         "ns_out_dtype": "bf16"}, indent=1))
+    print("muon steps", name, flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
@@ -298,6 +441,13 @@ def main() -> None:
         make_periods(ref, out)
     if args.only in (None, "dp"):
         make_dp(ref, out)
+    if args.only in (None, "ns"):
+        make_ns(ref, out)
+    if args.only in (None, "muon_steps"):
+        dp = np.load(out / "exact_dp.npz")
+        codebook = dp["hist_k256_forced/codebook"]
+        for name in ("muon_bf16", "muon_f32"):
+            make_muon_steps(ref, out, name, codebook)
     if args.only is None or args.only.startswith("traj"):
         dp = np.load(out / "exact_dp.npz")
         codebook = dp["hist_k256_forced/codebook"]

@@ -155,46 +155,77 @@ def test_adjacent_log_block_mean_difference_entry_point():
 
 
 def test_block_variance_and_cov_entry_points():
+    """Against the oracle's float64 restatement of the reference's CUDA scorers
+    (period_variance_kernel.cu:13-106): the kernels sum each block in float32, so
+    each block variance may differ by the float32 summation bound
+    2 P 2^-24 (E[x^2] + 2 mean^2)."""
     from gefen_amd.kernels.period_variance import (average_within_block_coefficient_of_variation_cuda_kernel,
                                                    average_within_block_variance_cuda_kernel)
 
-    g = syn.round_to(syn.row_scaled_normal(3, 3, 50, 64, -7, -2), "f32").reshape(-1)
-    t = gu.to_dev(g, "f32")
-    x = (g.astype(np.float64) ** 2).reshape(50, 64)
-    var = (x * x).mean(1) - x.mean(1) ** 2
-    ref = np.sqrt(np.maximum(var, 0).mean())
-    got = average_within_block_variance_cuda_kernel(t, 64, input_is_squared=False)
-    assert abs(got - ref) <= 1e-4 * ref
-    ref_cov = (np.sqrt(np.maximum(var, 0)) / x.mean(1)).mean()
-    got = average_within_block_coefficient_of_variation_cuda_kernel(t, 64, input_is_squared=False)
-    assert abs(got - ref_cov) <= 1e-4 * ref_cov
+    for dt, rows, period in (("f32", 50, 64), ("bf16", 40, 300), ("f16", 30, 2048)):
+        g = syn.round_to(syn.row_scaled_normal(3, rows, rows, period, -7, -2), dt).reshape(-1)
+        t = gu.to_dev(g, dt)
+        x = (orc.to_f32(g, dt) ** 2).astype(np.float64).reshape(rows, period)
+        m, m2 = x.mean(1), (x * x).mean(1)
+        var = np.maximum(m2 - m * m, 0)
+        dvar = 2 * period * 2.0 ** -24 * (m2 + 2 * m * m)
+        ref = orc.block_variance(g, dt, period, False, False)[0]
+        got = average_within_block_variance_cuda_kernel(t, period, input_is_squared=False)
+        assert abs(got - ref) <= dvar.mean() / (2 * ref) + 1e-15, (dt, got, ref)
+        cov = orc.block_variance(g, dt, period, False, True)
+        got = average_within_block_coefficient_of_variation_cuda_kernel(t, period, input_is_squared=False)
+        # d(sqrt(var)/m) <= dvar / (2 sqrt(var) m) + sqrt(var) dm / m^2, dm <= P 2^-24 m
+        dcov = (dvar / (2 * np.sqrt(np.maximum(var, 1e-300)) * m) + np.sqrt(var) * period * 2.0 ** -24 / m).mean()
+        assert abs(got - cov[0] / cov[1]) <= dcov, (dt, got, cov)
     with pytest.raises(RuntimeError, match="non-negative block means"):
         average_within_block_coefficient_of_variation_cuda_kernel(gu.to_dev(-np.ones(8, np.float32), "f32"), 4,
                                                                   input_is_squared=True)
 
 
-def test_lloyd_accumulate_and_mse():
+@pytest.mark.parametrize("case", ["plain", "nonfinite", "beyond_last"])
+def test_lloyd_accumulate_and_mse(case):
+    """gefen_lloyd_accumulate / gefen_lloyd_mse against the oracle's restatement of
+    the reference's CUDA semantics (lloyd_max_fused_kernel.cu:17-195): counts
+    bit-exact, float32 sums within the summation bound n_k 2^-24 sum|x|_k.
+    "nonfinite": NaN elements (the block absmax skips them, the element counts at
+    index 0) and an inf element; "beyond_last": a codebook ending below the
+    largest normalised value with a repeated last entry."""
     from gefen_amd.kernels.lloyd_max_fused import gefen_lloyd_accumulate_cuda, gefen_lloyd_mse_cuda
 
     data, _ = load("exact_dp")
     cb = data["hist_k256_forced/codebook"]
-    g = syn.round_to(syn.row_scaled_normal(6, 6, 30, 128, -14, -4), "f32").reshape(-1)
-    x = g.reshape(30, 128) / np.abs(g.reshape(30, 128)).max(1, keepdims=True)
-    idx = orc.nearest(cb, x.astype(np.float32).reshape(-1))
-    sums = torch.zeros(256, dtype=torch.float32, device="cuda:0")
-    counts = torch.zeros(256, dtype=torch.int64, device="cuda:0")
+    period, rows = 128, 30
+    g = syn.round_to(syn.row_scaled_normal(6, 6, rows, period, -14, -4), "f32").reshape(-1).copy()
+    if case == "nonfinite":
+        g[3 * period + 5] = np.nan
+        g[3 * period + 70] = np.nan
+        g[8 * period + 1] = np.inf
+        g[12 * period:13 * period] = 0.0
+    if case == "beyond_last":
+        cb = np.concatenate([cb[:200], cb[199:200]]).astype(np.float32)  # ends at cb[199] < 1, repeated
+    sums = torch.zeros(cb.size, dtype=torch.float32, device="cuda:0")
+    counts = torch.zeros(cb.size, dtype=torch.int64, device="cuda:0")
     cbd = torch.from_numpy(cb).to("cuda:0")
-    gefen_lloyd_accumulate_cuda(gu.to_dev(g, "f32"), cbd, 128, sums, counts)
-    np.testing.assert_array_equal(counts.cpu().numpy(), np.bincount(idx, minlength=256))
-    ref_sums = np.bincount(idx, weights=x.reshape(-1).astype(np.float64), minlength=256)
-    np.testing.assert_allclose(sums.cpu().numpy(), ref_sums, rtol=1e-4, atol=1e-5)
+    gefen_lloyd_accumulate_cuda(gu.to_dev(g, "f32"), cbd, period, sums, counts)
+    ref_sums, ref_counts = orc.lloyd_accumulate(g, "f32", period, cb)
+    np.testing.assert_array_equal(counts.cpu().numpy(), ref_counts)
+    got = sums.cpu().numpy().astype(np.float64)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref_sums))
+    ok = ~np.isnan(ref_sums)
+    # |x| <= 1, so sum|x|_k <= n_k: float32 summation in any order stays within n_k^2 2^-24
+    bound = ref_counts[ok].astype(np.float64) ** 2 * 2.0 ** -24
+    assert np.all(np.abs(got[ok] - ref_sums[ok]) <= bound)
+    new = (cb * np.float32(0.97)).astype(np.float32)
     mn = torch.zeros(1, dtype=torch.float32, device="cuda:0")
     mo = torch.zeros(1, dtype=torch.float32, device="cuda:0")
-    gefen_lloyd_mse_cuda(gu.to_dev(g, "f32"), cbd, cbd, 128, mn, mo)
-    err = x.reshape(-1) - cb[idx]
-    np.testing.assert_allclose(mn.item(), (err.astype(np.float64) ** 2).sum(), rtol=1e-4)
-    orig = err.reshape(30, 128) * np.abs(g.reshape(30, 128)).max(1, keepdims=True)
-    np.testing.assert_allclose(mo.item(), (orig.astype(np.float64) ** 2).sum(), rtol=1e-4)
+    gefen_lloyd_mse_cuda(gu.to_dev(g, "f32"), cbd, torch.from_numpy(new).to("cuda:0"), period, mn, mo)
+    rn, ro = orc.lloyd_mse(g, "f32", period, cb, new)
+    if case == "nonfinite":
+        assert np.isnan(mn.item()) and np.isnan(ro) and np.isnan(rn) and np.isnan(mo.item())
+    else:
+        n = g.size
+        assert abs(mn.item() - rn) <= n * 2.0 ** -24 * rn
+        assert abs(mo.item() - ro) <= n * 2.0 ** -24 * ro
 
 
 @pytest.mark.parametrize("dt,period", [("bf16", 64), ("f32", 32), ("bf16", 5000)])

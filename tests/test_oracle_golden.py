@@ -199,3 +199,75 @@ def test_given_vmean_and_given_stepsize_updates_equal_the_step(dt, sdt, period):
             np.testing.assert_array_equal(st[o].m_magnitude, a.m_magnitude)
             np.testing.assert_array_equal(p[o], p["a"])
         assert int(a.m_codebook.astype(np.int64).sum()) > 0
+
+
+# ------------------------------------------------------------------ Lloyd-Max / block variance (CUDA semantics)
+def _lloyd_brute(g, period, cb):
+    """Independent restatement of lloyd_max_fused_kernel.cu:17-107 for a sorted
+    codebook with distinct entries: the nearest codeword with ties to the lower
+    index, NaN to index 0; the block absmax ignores NaN."""
+    x = g.reshape(-1, period).astype(np.float32)
+    absmax = np.nanmax(np.abs(x), axis=1, keepdims=True)
+    absmax = np.where(np.isnan(absmax), 0, absmax).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        xn = np.where(absmax > 0, x / absmax, np.float32(0)).astype(np.float32).reshape(-1)
+    d = np.abs(xn[:, None].astype(np.float64) - cb[None, :].astype(np.float64))
+    idx = np.argmin(np.where(np.isnan(d), np.inf, d), axis=1)
+    idx[np.isnan(xn)] = 0
+    return xn, idx
+
+
+def test_lloyd_oracle_matches_brute_force():
+    from gefen_amd import synthetic as syn
+
+    data, _ = load("exact_dp")
+    for cb in (data["hist_k256_forced/codebook"], data["hist_k16_free/codebook"]):
+        assert np.all(np.diff(cb) > 0)
+        g = syn.round_to(syn.row_scaled_normal(7, 1, 24, 96, -12, -3), "f32").reshape(-1).copy()
+        g[5 * 96 + 7] = np.nan            # a NaN element: skipped by the absmax, counted at index 0
+        g[9 * 96:10 * 96] = 0.0           # a zero block: every x is 0
+        g[11 * 96 + 3] = np.inf           # an inf element: absmax inf, x = 0 or NaN
+        xn, idx = _lloyd_brute(g, 96, cb)
+        sums, counts = orc.lloyd_accumulate(g, "f32", 96, cb)
+        np.testing.assert_array_equal(counts, np.bincount(idx, minlength=cb.size))
+        ref = np.bincount(idx, weights=xn.astype(np.float64), minlength=cb.size)
+        np.testing.assert_array_equal(np.isnan(sums), np.isnan(ref))
+        ok = ~np.isnan(ref)
+        np.testing.assert_allclose(sums[ok], ref[ok], rtol=1e-12, atol=1e-12)
+        new = (cb * np.float32(0.99)).astype(np.float32)
+        mn, mo = orc.lloyd_mse(g, "f32", 96, cb, new)
+        assert np.isnan(mn) and np.isnan(mo)   # the NaN element's error is NaN
+        g2 = g.copy()
+        g2[np.isnan(g2) | np.isinf(g2)] = 0.5
+        xn, idx = _lloyd_brute(g2, 96, cb)
+        amax = np.repeat(np.abs(g2.reshape(-1, 96)).max(1), 96).astype(np.float32)
+        err = (xn - new[idx]).astype(np.float32)
+        mn, mo = orc.lloyd_mse(g2, "f32", 96, cb, new)
+        # each squared error is a float32 product (lines 173-176); sums in double
+        assert abs(mn - float((err * err).astype(np.float64).sum())) <= 1e-12 * max(mn, 1e-30)
+        oe = (err * amax).astype(np.float32)
+        assert abs(mo - float((oe * oe).astype(np.float64).sum())) <= 1e-12 * max(mo, 1e-30)
+
+
+def test_lloyd_oracle_index_beyond_the_last_codeword():
+    """x above the last codeword: the reference compares the last two entries, so
+    a duplicated last codeword takes the lower index (lloyd_max_fused_kernel.cu:33-47)."""
+    cb = np.array([-0.5, 0.0, 0.25, 0.25], np.float32)
+    g = np.array([1.0, 0.5, -1.0, 0.0], np.float32)   # absmax 1: x = 1, 0.5, -1, 0
+    _, counts = orc.lloyd_accumulate(g, "f32", 4, cb)
+    assert counts.tolist() == [1, 1, 2, 0]
+
+
+def test_block_variance_oracle_matches_closed_form():
+    from gefen_amd import synthetic as syn
+
+    g = syn.round_to(syn.row_scaled_normal(3, 3, 50, 64, -7, -2), "f32").reshape(-1)
+    x = (g.astype(np.float32) ** 2).astype(np.float64).reshape(50, 64)
+    var = np.maximum((x * x).mean(1) - x.mean(1) ** 2, 0)
+    out = orc.block_variance(g, "f32", 64, False, False)
+    np.testing.assert_allclose(out[0], np.sqrt(var.mean()), rtol=1e-12)
+    out = orc.block_variance(g, "f32", 64, False, True)
+    np.testing.assert_allclose(out[0], (np.sqrt(var) / x.mean(1)).sum(), rtol=1e-12)
+    assert out[1] == 50 and out[2] == 0
+    out = orc.block_variance(-np.ones(8, np.float32), "f32", 4, True, True)
+    assert out[2] == 2 and out[1] == 0
