@@ -185,12 +185,17 @@ class PlanCore {
     size_t size() const { return params_.size(); }
 
    private:
-    // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group
+    // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group.
+    // A tensor lr of another dtype than float64 with weight decay > 0 is refused:
+    // torch forms that decay factor in the tensor's dtype (the Python step applies
+    // it before the launch), where the kernel's double expression would differ.
     bool group_hyper(PyObject* group, std::array<double, 5>& h) {
         PyObject* keys[5] = {key_lr_, key_beta1_, key_beta2_, key_eps_, key_wd_};
+        bool lr_tensor = false;
         for (int c = 0; c < 5; ++c) {
             PyObject* v = PyDict_GetItem(group, keys[c]);
             if (!v) return false;
+            if (c == 0) lr_tensor = THPVariable_Check(v) && THPVariable_Unpack(v).scalar_type() != at::kDouble;
             if (PyFloat_CheckExact(v)) {
                 h[c] = PyFloat_AS_DOUBLE(v);
                 continue;
@@ -203,7 +208,7 @@ class PlanCore {
             h[c] = PyFloat_AS_DOUBLE(f);
             Py_DECREF(f);
         }
-        return true;
+        return !(lr_tensor && h[4] > 0.0);
     }
 
     int device_type_ = -1, device_index_ = -1;

@@ -310,6 +310,8 @@ class _StepPlan:
                                      self.steps.ctypes.data):
                 return None
             return t
+        if _tensor_lr_with_decay(self.distinct):
+            return None
         steps = _plan_checks_python(self, opt)
         if steps is None:
             return None
@@ -390,6 +392,18 @@ def _plan_checks_python(plan, opt):
         st["step"] = step
         steps.append(step)
     return steps
+
+
+def _decay_from_lr_tensor(lr, weight_decay) -> bool:
+    """Weight decay with a tensor lr whose dtype is not float64: torch forms the
+    factor 1 - lr * wd in that dtype (fl32(1 - fl32(lr * fl32(wd))) for float32),
+    not in double as the kernels do, so torch applies it before the launch."""
+    return weight_decay > 0.0 and torch.is_tensor(lr) and lr.dtype != torch.float64
+
+
+def _tensor_lr_with_decay(groups) -> bool:
+    """A group whose decay factor torch forms (no cached plan applies then)."""
+    return any(_decay_from_lr_tensor(g["lr"], g["weight_decay"]) for g in groups)
 
 
 def _distinct(objs):
@@ -814,8 +828,8 @@ class Gefen(torch.optim.Optimizer):
             period = st["automatic_period"]
             st["step"] += 1
             step = st["step"]
-            lr = group["lr"]
-            lr = float(lr.item()) if torch.is_tensor(lr) else float(lr)
+            lr_group = group["lr"]
+            lr = float(lr_group.item()) if torch.is_tensor(lr_group) else float(lr_group)
             b1, b2 = group["beta1"], group["beta2"]
             plain = plain and local_p is p and grad is p.grad and grad.is_contiguous()
             flat_grad = grad.reshape(-1)
@@ -833,6 +847,13 @@ class Gefen(torch.optim.Optimizer):
                 raise ValueError("Expected grad_view dtype {} to match p dtype {}.".format(flat_grad.dtype,
                                                                                            fused_p.dtype))
             keep.append(flat_grad)
+            wd = group["weight_decay"]
+            if _decay_from_lr_tensor(lr_group, wd):
+                # p.mul_(1 - lr * wd) as gefen.py:1280-1281 evaluates it for a tensor lr
+                # (a double formula misses fl32(1 - fl32(lr * wd)) in ~1% of cases);
+                # the kernel then skips its own decay
+                fused_p.mul_(1 - lr_group * wd)
+                wd = 0.0
             t = tasks[i]
             t["p"] = fused_p.data_ptr()
             t["grad"] = flat_grad.data_ptr()
@@ -849,7 +870,7 @@ class Gefen(torch.optim.Optimizer):
             t["beta2"] = b2
             t["lr"] = lr
             t["eps"] = group["eps"]
-            t["weight_decay"] = group["weight_decay"]
+            t["weight_decay"] = wd
             t["bias_correction_1"] = 1 - b1 ** step
             t["bias_correction_2"] = 1 - b2 ** step
         dev = items[0][3].device

@@ -19,7 +19,7 @@ import torch.nn as nn
 
 from gefen_amd import _lib
 from gefen_amd.gefen import (Gefen, _DTYPE_CODE, _distinct, _gefen_host, _plan_checks_python,
-                             automatic_partition_view)
+                             _decay_from_lr_tensor, _tensor_lr_with_decay, automatic_partition_view)
 
 EPS = 1e-7
 DEFAULT_A = 3.4445
@@ -236,8 +236,8 @@ class GefenMuon(Gefen):
                 update = _zeropower_via_newtonschulz(out.view_as(grad), group["ns_coefficients"], group["ns_steps"],
                                                      group["eps"]).contiguous()
             keep.append(update)
-            lr = group["lr"]
-            lr = float(lr.item()) if torch.is_tensor(lr) else float(lr)
+            lr_group = group["lr"]
+            lr = float(lr_group.item()) if torch.is_tensor(lr_group) else float(lr_group)
             adjusted = _adjust_lr(lr, group["adjust_lr_fn"], p.shape)
             if local_p.is_contiguous():
                 target = local_p
@@ -248,6 +248,12 @@ class GefenMuon(Gefen):
                 raise ValueError("GefenMuon fused update requires a contiguous parameter tensor for {}.".format(
                     group["name"]))
             keep.append(target)
+            wd = group["weight_decay"]
+            if _decay_from_lr_tensor(lr_group, wd):
+                # p.mul_(1 - lr * wd) with a tensor lr (gefen_muon.py:325-326): the factor
+                # in the tensor's dtype, as torch forms it; the apply kernel skips its decay
+                target.mul_(1 - lr_group * wd)
+                wd = 0.0
             t = apply[i]
             t["p"] = target.data_ptr()
             t["update"] = update.data_ptr()
@@ -255,7 +261,7 @@ class GefenMuon(Gefen):
             t["param_dtype"] = _DTYPE_CODE[target.dtype]
             t["transposed"] = 1 if grad.size(0) > grad.size(1) else 0
             t["lr"] = lr
-            t["weight_decay"] = group["weight_decay"]
+            t["weight_decay"] = wd
             t["adjusted_lr"] = adjusted
         with torch.cuda.device(dev):
             rc = lib.gefen_muon_apply_tasks(apply.ctypes.data, len(items), torch.cuda.current_stream(dev).cuda_stream)
@@ -329,6 +335,8 @@ class _MuonPlan:
         return out
 
     def refresh(self, opt) -> bool:
+        if _tensor_lr_with_decay(self.distinct):
+            return False
         settings = self._settings()
         if any(a[1] != b[1] for a, b in zip(settings, self.settings)):
             return False
@@ -362,11 +370,17 @@ class _MuonPlan:
             stream = torch.cuda.current_stream(self.device).cuda_stream
             _lib.check(lib.gefen_muon_tasks(self.mtasks.ctypes.data, len(self.mtasks), tables.data_ptr(), stream),
                        "gefen_muon_tasks")
+            # newton_schulz_batched may return its input (a bf16 copy of a non-bf16
+            # stack, with an even or zero step count): every input and result stays
+            # referenced here until the launch that reads them is enqueued
+            keep = []
             for key, idx, buf, work in self.stacks:
                 coeffs, steps, eps = key[3], key[4], key[5]
                 x = buf if key[2] == torch.bfloat16 else buf.bfloat16()
                 res = newton_schulz_batched(x, coeffs, steps, eps, work=work)
+                keep.append((x, res))
                 slot_bytes = res[0].numel() * res.element_size()
                 self.apply["update"][idx] = res.data_ptr() + np.arange(len(idx), dtype=np.uint64) * slot_bytes
             _lib.check(lib.gefen_muon_apply_tasks(self.apply.ctypes.data, len(self.apply), stream),
                        "gefen_muon_apply_tasks")
+            del keep

@@ -196,5 +196,8 @@ def test_plan_core_checks_and_commits_only_when_the_plan_applies():
     unchanged_after(lambda: states[2].__setitem__("vmean", vm.clone()), lambda: states[2].__setitem__("vmean", vm))
     unchanged_after(lambda: states[0].__setitem__("step", torch.tensor(5)), lambda: states[0].__setitem__("step", 9))
     unchanged_after(lambda: groups[1].__setitem__("lr", "fast"), lambda: groups[1].__setitem__("lr", 2e-3))
-    assert [st["step"] for st in states] == [11, 12, 12] and steps.tolist() == [11, 12, 12]
-    assert table["bias_correction_1"].tolist() == [1 - 0.9 ** 11, 1 - 0.9 ** 12, 1 - 0.8 ** 12]
+    # a float32 lr tensor with weight decay: torch forms that decay factor (no plan)
+    unchanged_after(lambda: groups[1].__setitem__("lr", torch.tensor(2e-3, dtype=torch.float32)),
+                    lambda: groups[1].__setitem__("lr", 2e-3))
+    assert [st["step"] for st in states] == [12, 13, 13] and steps.tolist() == [12, 13, 13]
+    assert table["bias_correction_1"].tolist() == [1 - 0.9 ** 12, 1 - 0.9 ** 13, 1 - 0.8 ** 13]
