@@ -1246,16 +1246,23 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
         if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
             return launch_status("gefen step fork");
     }
+    int rc = GEFEN_OK;
     for (const Launch& L : launches) {
         hipStream_t ls = (side && L.elems < kSmallLaunchElems) ? side->s : st;
         hipError_t e = dispatch_step(L.key, L.b, L.wg, ls);
-        if (e != hipSuccess) return hip_status(e, "gefen step launch");
+        if (e != hipSuccess) {
+            rc = hip_status(e, "gefen step launch");
+            break;
+        }
     }
+    // join even after a failed launch: st must stay ordered after the side-stream
+    // launches already queued (they read the stepsize tables and write parameters)
     if (side) {
-        if (hipEventRecord(side->join, side->s) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
-            return launch_status("gefen step join");
+        const hipError_t e1 = hipEventRecord(side->join, side->s);
+        const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(st, side->join, 0) : e1;
+        if (e2 != hipSuccess && rc == GEFEN_OK) rc = hip_status(e2, "gefen step join");
     }
-    return GEFEN_OK;
+    return rc;
 }
 
 // Build the StepTask of one tensor.  mode / stepsize select the stepsize source.
@@ -1312,50 +1319,152 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     return GEFEN_OK;
 }
 
-// Build the stepsize tables of the period-one tasks with a 16-bit state (one
-// table per distinct (dtype, sqrt(bc2), eps, 1/bc1): the 384-entry square-root
-// table for bf16, the 32768-entry stepsize table for f16); *buf owns them until
-// the launches that read them are enqueued.
-int prepare_luts(std::vector<PendingStep>& pend, hipStream_t st, void** buf) {
-    struct LutKey { int s; float a, b, c; };
-    std::vector<LutKey> keys;
-    std::vector<int> which(pend.size(), -1);
+// Stepsize tables of the period-one tasks with a 16-bit state: one per distinct
+// (state dtype, sqrt(bc2), eps, 1/bc1); the 384-entry square-root table for
+// bf16 (k_build_root), the 32768-entry stepsize table for f16 (k_build_lut).
+struct LutPlan {
+    struct KeyT { int s; float a, b, c; };
+    std::vector<KeyT> keys;
+    std::vector<size_t> off;   // float offset of each key's table
+    std::vector<int> which;    // key of each pending task, -1 if it takes no table
+    size_t total = 0;          // floats of all tables
+};
+
+constexpr size_t kRootSlot = kRootTab;  // 1536 bytes: 256-byte aligned slots
+constexpr size_t kLutSlot = 32768;
+static_assert(kRootSlot % 64 == 0 && kLutSlot % 64 == 0, "table slots keep 256-byte alignment");
+
+void plan_luts(const std::vector<PendingStep>& pend, LutPlan& lp) {
+    lp.which.assign(pend.size(), -1);
     for (size_t i = 0; i < pend.size(); ++i) {
         const Key& k = pend[i].key;
         if (!k.p1 || k.s == GEFEN_F32) continue;
         const StepTask& t = pend[i].task;
         int found = -1;
-        for (size_t j = 0; j < keys.size(); ++j)
-            if (keys[j].s == k.s && memcmp(&keys[j].a, &t.sqrt_bc2, 4) == 0 && memcmp(&keys[j].b, &t.eps, 4) == 0 &&
-                memcmp(&keys[j].c, &t.inv_bc1, 4) == 0)
+        for (size_t j = 0; j < lp.keys.size(); ++j)
+            if (lp.keys[j].s == k.s && memcmp(&lp.keys[j].a, &t.sqrt_bc2, 4) == 0 &&
+                memcmp(&lp.keys[j].b, &t.eps, 4) == 0 && memcmp(&lp.keys[j].c, &t.inv_bc1, 4) == 0)
                 found = (int)j;
         if (found < 0) {
-            found = (int)keys.size();
-            keys.push_back(LutKey{k.s, t.sqrt_bc2, t.eps, t.inv_bc1});
+            found = (int)lp.keys.size();
+            lp.keys.push_back(LutPlan::KeyT{k.s, t.sqrt_bc2, t.eps, t.inv_bc1});
+            lp.off.push_back(lp.total);
+            lp.total += k.s == GEFEN_BF16 ? kRootSlot : kLutSlot;
         }
-        which[i] = found;
+        lp.which[i] = found;
     }
-    *buf = nullptr;
-    if (keys.empty()) return GEFEN_OK;
-    hipError_t e = hipMallocAsync(buf, keys.size() * 32768 * sizeof(float), st);
-    if (e != hipSuccess) return hip_status(e, "hipMallocAsync(stepsize tables)");
-    float* base = static_cast<float*>(*buf);
-    for (size_t j = 0; j < keys.size(); ++j) {
+}
+
+// Build the planned tables at base (lp.total floats of device memory) on st and
+// point the tasks at them.
+int build_luts(std::vector<PendingStep>& pend, const LutPlan& lp, float* base, hipStream_t st) {
+    for (size_t j = 0; j < lp.keys.size(); ++j) {
         StepTask t;
         memset(&t, 0, sizeof(t));
-        t.sqrt_bc2 = keys[j].a;
-        t.eps = keys[j].b;
-        t.inv_bc1 = keys[j].c;
-        if (keys[j].s == GEFEN_BF16)
-            hipLaunchKernelGGL(k_build_root, dim3((kRootTab + 255) / 256), dim3(256), 0, st, base + j * 32768, t);
+        t.sqrt_bc2 = lp.keys[j].a;
+        t.eps = lp.keys[j].b;
+        t.inv_bc1 = lp.keys[j].c;
+        if (lp.keys[j].s == GEFEN_BF16)
+            hipLaunchKernelGGL(k_build_root, dim3((kRootTab + 255) / 256), dim3(256), 0, st, base + lp.off[j], t);
         else
-            hipLaunchKernelGGL(k_build_lut<f16_t>, dim3(128), dim3(256), 0, st, base + j * 32768, t);
+            hipLaunchKernelGGL(k_build_lut<f16_t>, dim3(128), dim3(256), 0, st, base + lp.off[j], t);
         int rc = launch_status("gefen stepsize table");
         if (rc) return rc;
     }
     for (size_t i = 0; i < pend.size(); ++i)
-        if (which[i] >= 0) pend[i].task.lut = base + (size_t)which[i] * 32768;
+        if (lp.which[i] >= 0) pend[i].task.lut = base + lp.off[(size_t)lp.which[i]];
     return GEFEN_OK;
+}
+
+// Device of a stream (the current device for the null stream).
+int stream_device(hipStream_t st, int* dev) {
+    if (hipGetDevice(dev) != hipSuccess) return launch_status("hipGetDevice");
+    if (st) {
+        hipDevice_t sd = -1;
+        hipError_t e = hipStreamGetDevice(st, &sd);
+        if (e != hipSuccess) return hip_status(e, "hipStreamGetDevice");
+        *dev = sd;
+    }
+    if (*dev < 0 || *dev >= kMaxDevices) return fail_inval("device %d out of range", *dev);
+    return GEFEN_OK;
+}
+
+// Makes `dev` current for its lifetime when it is not.
+struct DeviceScope {
+    int prev = -1;
+    explicit DeviceScope(int dev) {
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur != dev && hipSetDevice(dev) == hipSuccess) prev = cur;
+    }
+    ~DeviceScope() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+// Library-owned stepsize-table memory of a device, kept between calls and grown
+// when a call needs more.  `done` is recorded on the stream of the last call
+// after its launches; a call on another stream waits for it before rewriting
+// the tables, so calls on different streams stay ordered.
+struct LutPool {
+    std::mutex m;
+    float* buf = nullptr;
+    size_t cap = 0;  // floats
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool recorded = false;
+};
+LutPool g_lut_pool[kMaxDevices];
+
+// Stepsize tables in the device's pool, then the step launches.
+int run_steps_pooled(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st) {
+    LutPlan lp;
+    plan_luts(pend, lp);
+    if (lp.keys.empty()) return flush_steps(pend, tables, st);
+    int dev = 0;
+    int rc = stream_device(st, &dev);
+    if (rc) return rc;
+    LutPool& pool = g_lut_pool[dev];
+    std::lock_guard<std::mutex> lock(pool.m);
+    if (pool.cap < lp.total || !pool.done) {
+        DeviceScope scope(dev);
+        if (!pool.done) {
+            hipError_t e = hipEventCreateWithFlags(&pool.done, hipEventDisableTiming);
+            if (e != hipSuccess) {
+                pool.done = nullptr;
+                return hip_status(e, "hipEventCreate(stepsize tables)");
+            }
+        }
+        if (pool.cap < lp.total) {
+            if (pool.buf) {
+                if (pool.recorded) (void)hipEventSynchronize(pool.done);
+                (void)hipFree(pool.buf);
+                pool.buf = nullptr;
+                pool.cap = 0;
+            }
+            const size_t want = std::max<size_t>(lp.total, 4 * kLutSlot);
+            hipError_t e = hipMalloc(reinterpret_cast<void**>(&pool.buf), want * sizeof(float));
+            if (e != hipSuccess) {
+                pool.buf = nullptr;
+                return hip_status(e, "hipMalloc(stepsize tables)");
+            }
+            pool.cap = want;
+        }
+    }
+    if (pool.recorded && pool.last != st) {
+        hipError_t e = hipStreamWaitEvent(st, pool.done, 0);
+        if (e != hipSuccess) return hip_status(e, "hipStreamWaitEvent(stepsize tables)");
+    }
+    rc = build_luts(pend, lp, pool.buf, st);
+    if (rc == GEFEN_OK) rc = flush_steps(pend, tables, st);
+    // recorded after the join of the side stream: covers every launch that reads the tables
+    hipError_t e = hipEventRecord(pool.done, st);
+    if (e == hipSuccess) {
+        pool.recorded = true;
+        pool.last = st;
+    } else if (rc == GEFEN_OK) {
+        rc = hip_status(e, "hipEventRecord(stepsize tables)");
+    }
+    return rc;
 }
 
 int check_step_task(const gefen_step_task& t) {
@@ -1412,12 +1521,7 @@ extern "C" int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const 
         if (rc) return rc;
         pend.push_back(ps);
     }
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    void* luts = nullptr;
-    int rc = prepare_luts(pend, st, &luts);
-    if (rc == GEFEN_OK) rc = flush_steps(pend, static_cast<const CodebookTables*>(tables), st);
-    if (luts) (void)hipFreeAsync(luts, st);
-    return rc;
+    return run_steps_pooled(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
 }
 
 static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign, void* mag,
@@ -1472,11 +1576,7 @@ static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_
         return e == hipSuccess ? GEFEN_OK : hip_status(e, "gefen packed step launch");
     }
     std::vector<PendingStep> pend(1, ps);
-    void* luts = nullptr;
-    rc = prepare_luts(pend, st, &luts);
-    if (rc == GEFEN_OK) rc = flush_steps(pend, static_cast<const CodebookTables*>(tt.ptr), st);
-    if (luts) (void)hipFreeAsync(luts, st);
-    return rc;
+    return run_steps_pooled(pend, static_cast<const CodebookTables*>(tt.ptr), st);
 }
 
 extern "C" int gefen_automatic_fused_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign,
