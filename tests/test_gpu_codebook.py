@@ -7,6 +7,7 @@ import pytest
 import torch
 
 import gpu_util as gu
+import traj_util as tu
 from golden_util import load
 from gefen_amd import synthetic as syn
 from oracle import oracle as orc
@@ -163,7 +164,7 @@ def test_block_variance_and_cov_entry_points():
                                                    average_within_block_variance_cuda_kernel)
 
     for dt, rows, period in (("f32", 50, 64), ("bf16", 40, 300), ("f16", 30, 2048)):
-        g = syn.round_to(syn.row_scaled_normal(3, rows, rows, period, -7, -2), dt).reshape(-1)
+        g = tu.bits(syn.round_to(syn.row_scaled_normal(3, rows, rows, period, -7, -2), dt).reshape(-1))
         t = gu.to_dev(g, dt)
         x = (orc.to_f32(g, dt) ** 2).astype(np.float64).reshape(rows, period)
         m, m2 = x.mean(1), (x * x).mean(1)
