@@ -39,6 +39,7 @@ SIGNATURES = {
         I32, [P, P, I32, P, P, I32, P, I32, P, I32, I64, I64, DBL, DBL, DBL, DBL, DBL, DBL, P]),
     "gefen_automatic_muon_momentum": (I32, [P, I32, P, P, I32, P, I32, P, I32, I64, I64, DBL, P]),
     "gefen_step_tasks": (I32, [P, I32, P, P]),
+    "gefen_step_tasks_noalloc": (I32, [P, I32, P, P]),
     "gefen_muon_tasks": (I32, [P, I32, P, P]),
     "gefen_ns_prepare": (I32, [P, P, I32, I32, I32, DBL, P]),
     "gefen_muon_apply_tasks": (I32, [P, I32, P]),

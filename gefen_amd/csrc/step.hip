@@ -23,6 +23,15 @@
 #include "capi_internal.h"
 #include "common.h"
 
+// Scratch buffer of gefen_step_tasks_noalloc: the stepsize tables of one call,
+// at most kNoAllocScratchFloats floats (1 MiB per device, held until the process
+// ends).  Host code never passes `scratch` itself to a kernel or a copy: on the
+// host the name is only a stand-in for the device variable.  Its device address
+// comes from hipGetSymbolAddress, once per device with that device current
+// (gefen::scratch_for_device), and only that address is used.
+static constexpr size_t kNoAllocScratchFloats = size_t(1) << 18;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace gefen {
 
 #ifndef GEFEN_MUON_TAB_LOG2
@@ -1201,7 +1210,10 @@ SideStream* side_stream(hipStream_t st) {
     return ss.s ? &ss : nullptr;
 }
 
-int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st) {
+// Launch every pending task.  allow_side = false keeps every launch on st (no
+// library-owned stream or event is created or used).
+int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st,
+                bool allow_side = true) {
     // group by kernel key, up to kMaxBatch tasks per launch
     struct Launch {
         Key key;
@@ -1239,7 +1251,7 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
     }
     bool any_small = false, any_large = false;
     for (const Launch& L : launches) (L.elems < kSmallLaunchElems ? any_small : any_large) = true;
-    SideStream* side = (any_small && any_large) ? side_stream(st) : nullptr;
+    SideStream* side = (allow_side && any_small && any_large) ? side_stream(st) : nullptr;
     std::unique_lock<std::mutex> lock;
     if (side) {
         lock = std::unique_lock<std::mutex>(side->m);
@@ -1467,6 +1479,25 @@ int run_steps_pooled(std::vector<PendingStep>& pend, const CodebookTables* table
     return rc;
 }
 
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device
+
+int scratch_for_device(int dev, float** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        DeviceScope scope(dev);
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess || cur != dev) return fail_inval("cannot make device %d current", dev);
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(::scratch));
+        if (e != hipSuccess || !ptr) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                       "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return GEFEN_OK;
+}
+
 int check_step_task(const gefen_step_task& t) {
     if (t.numel < 0) return fail_inval("numel must be non-negative");
     if (!valid_pair(t.param_dtype, t.state_dtype))
@@ -1522,6 +1553,42 @@ extern "C" int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const 
         pend.push_back(ps);
     }
     return run_steps_pooled(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int gefen_step_tasks_noalloc(const gefen_step_task* tasks, int ntasks, const void* tables,
+                                        gefen_stream_t stream) {
+    if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
+    if (!tables) return fail_inval("null codebook tables");
+    std::vector<PendingStep> pend;
+    pend.reserve(ntasks);
+    for (int i = 0; i < ntasks; ++i) {
+        int rc = check_step_task(tasks[i]);
+        if (rc) return rc;
+        if (tasks[i].numel == 0) continue;
+        PendingStep ps;
+        rc = make_step_task(tasks[i], kVmeanUpdate, nullptr, ps);
+        if (rc) return rc;
+        pend.push_back(ps);
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    LutPlan lp;
+    plan_luts(pend, lp);
+    if (lp.total > kNoAllocScratchFloats)
+        return fail_inval("the stepsize tables of this call need %zu bytes, more than the %zu-byte scratch buffer "
+                          "(at most %zu f16-state or %zu bf16-state (sqrt(bc2), eps, 1/bc1) settings per call)",
+                          lp.total * sizeof(float), kNoAllocScratchFloats * sizeof(float), kNoAllocScratchFloats / kLutSlot,
+                          kNoAllocScratchFloats / kRootSlot);
+    if (!lp.keys.empty()) {
+        int dev = 0;
+        int rc = stream_device(st, &dev);
+        if (rc) return rc;
+        float* base = nullptr;
+        rc = scratch_for_device(dev, &base);
+        if (rc) return rc;
+        rc = build_luts(pend, lp, base, st);
+        if (rc) return rc;
+    }
+    return flush_steps(pend, static_cast<const CodebookTables*>(tables), st, false);
 }
 
 static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign, void* mag,

@@ -132,6 +132,19 @@ typedef struct gefen_step_task {
 int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const void* tables,
                      gefen_stream_t stream);
 
+/* The same step as gefen_step_tasks, allocating nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The period-one stepsize tables of 16-bit states go to a library-owned static
+ * device buffer of 1 MiB per device (held until the process ends): at most 8
+ * distinct f16-state or 682 distinct bf16-state (sqrt(bias_correction_2), eps,
+ * 1/bias_correction_1) settings per call, else GEFEN_EINVAL before anything is
+ * launched.  Every launch runs on `stream` (no side stream).  Calls on one
+ * device share that buffer, which keeps the last call's tables: calls that
+ * overlap on one device (other streams, other threads) race. */
+int gefen_step_tasks_noalloc(const gefen_step_task* tasks, int ntasks, const void* tables,
+                             gefen_stream_t stream);
+
 /* GefenMuon momentum of many tensors with the Nesterov blend fused
  * (gefen_muon.py:302-316): out = D(D(q*mu) + g*(1-mu)) if nesterov, else q. */
 typedef struct gefen_muon_task {
