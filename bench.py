@@ -180,6 +180,25 @@ def bench_kernels(args, dev):
 
 
 
+def fill_grad(cfg, g, index, step=0, seed=2026):
+    """Gradient `index` of the config for `step` (0: the gradient of the first step,
+    stream = index; later steps use streams step * 100000 + index), in place:
+    "row": N(0,1) times a dyadic log-uniform scale per row in [2^-14, 2^-4] (GPT-2,
+    ~[6e-5, 6e-2]); "tensor": one scale per tensor in [2^-17, 2^-7] (~[7.6e-6, 7.8e-3]);
+    "muon": N(0, 1e-3) (2^-10 ~ 0.98e-3)."""
+    from gefen_amd import synthetic as syn
+
+    stream = index if step == 0 else step * 100_000 + index
+    n = g.numel()
+    if cfg["grad"] == "row":
+        cols = g.shape[-1] if g.dim() > 1 else n
+        syn.fill_device(g, seed, stream, syn.KIND_ROW_SCALED, cols=cols, e_lo=-14, e_hi=-4)
+    elif cfg["grad"] == "muon":
+        syn.fill_device(g, seed, stream, syn.KIND_ROW_SCALED, cols=n, e_lo=-10, e_hi=-10)
+    else:
+        syn.fill_device(g, seed, stream, syn.KIND_ROW_SCALED, cols=n, e_lo=-17, e_hi=-7)
+
+
 def build_problem(cfg, dev, seed=2026):
     from gefen_amd import synthetic as syn
 
@@ -188,14 +207,7 @@ def build_problem(cfg, dev, seed=2026):
         p = torch.empty(shape, dtype=cfg["dtype"], device=dev)
         syn.fill_device(p, seed, 1_000_000 + i, syn.KIND_NORMAL, mult=0.02)
         g = torch.empty(shape, dtype=cfg["dtype"], device=dev)
-        n = g.numel()
-        if cfg["grad"] == "row":
-            cols = shape[-1] if len(shape) > 1 else n
-            syn.fill_device(g, seed, i, syn.KIND_ROW_SCALED, cols=cols, e_lo=-14, e_hi=-4)
-        elif cfg["grad"] == "muon":
-            syn.fill_device(g, seed, i, syn.KIND_ROW_SCALED, cols=n, e_lo=-10, e_hi=-10)
-        else:
-            syn.fill_device(g, seed, i, syn.KIND_ROW_SCALED, cols=n, e_lo=-17, e_hi=-7)
+        fill_grad(cfg, g, i, 0, seed)
         p.requires_grad_(True)
         p.grad = g
         params.append((name, p))

@@ -248,6 +248,15 @@ def _resolve_find_period_backend(grad: torch.Tensor) -> str:
     return FIND_PERIOD_BACKEND
 
 
+def _flat_with_data(grad: torch.Tensor) -> torch.Tensor:
+    """grad.detach().reshape(-1), after touching its data: a gradient whose storage
+    is not allocated yet raises here, where the reference's first kernel call
+    would raise."""
+    flat = grad.detach().reshape(-1)
+    flat.data_ptr()
+    return flat
+
+
 def _local(tensor):
     if hasattr(tensor, "to_local"):
         tensor = tensor.to_local()
@@ -578,17 +587,19 @@ class Gefen(torch.optim.Optimizer):
         ppr = self._print_period_results_enabled()
         scorer = PeriodScorer(mode=1)
         for p, grad in items:
-            g = _local(grad).detach()
-            if g.device.type != "cuda":
-                raise ValueError("gefen_amd runs on HIP devices; a gradient is on {}".format(g.device))
+            work = _local(grad)
+            if work.device.type != "cuda":
+                raise ValueError("gefen_amd runs on HIP devices; a gradient is on {}".format(work.device))
             try:
-                flat = g.reshape(-1)
-            except RuntimeError as exc:  # FSDP lazily materialised gradient (gefen.py:789-810)
+                flat = _flat_with_data(work)
+            except RuntimeError as exc:
+                # a lazily materialised (FSDP) gradient: add_(0) allocates it, then
+                # the scores are taken again (gefen.py:789-810)
                 msg = str(exc)
                 if "data is not allocated yet" not in msg and "invalid python storage" not in msg:
                     raise
-                g.add_(0)
-                flat = g.reshape(-1)
+                work.add_(0)
+                flat = _flat_with_data(work)
             scorer.add(flat, self._max_period_for_param(p), ppr)
         return scorer.finish()
 

@@ -49,16 +49,23 @@ def words(key: np.uint64, start: int, count: int) -> np.ndarray:
         return splitmix64(np.uint64(key) + c * GAMMA)
 
 
+_CHUNK = 1 << 20  # elements per pass: keeps the temporaries in cache
+
+
 def normal(key: np.uint64, n: int, start: int = 0) -> np.ndarray:
     """n approximately N(0,1) float64 values (exact dyadic rationals)."""
-    w = words(key, 3 * start, 3 * n).reshape(n, 3)
-    s = np.zeros(n, dtype=np.int64)
+    out = np.empty(n, dtype=np.float64)
     mask = np.uint64(0xFFFF)
-    for j in range(3):
-        col = w[:, j]
-        for k in range(4):
-            s += ((col >> np.uint64(16 * k)) & mask).astype(np.int64)
-    return (2 * s - 12 * 65535).astype(np.float64) / 131072.0
+    for c0 in range(0, n, _CHUNK):
+        m = min(_CHUNK, n - c0)
+        w = words(key, 3 * (start + c0), 3 * m).reshape(m, 3)
+        s = np.zeros(m, dtype=np.int64)
+        for j in range(3):
+            col = w[:, j]
+            for k in range(4):
+                s += ((col >> np.uint64(16 * k)) & mask).astype(np.int64)
+        out[c0:c0 + m] = (2 * s - 12 * 65535).astype(np.float64) / 131072.0
+    return out
 
 
 def dyadic_scale(key: np.uint64, n: int, e_lo: int, e_hi: int) -> np.ndarray:

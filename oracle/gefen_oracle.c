@@ -347,24 +347,38 @@ int orc_histogram(int gdt, const void* g, int64_t n, int64_t period, int bins,
     if (period <= 0 || n % period != 0 || bins <= 0) return 1;
     const float bw = (float)(2.0 / (double)bins);
     const int64_t rows = n / period;
-    for (int64_t r = 0; r < rows; ++r) {
-        float amax = 0.0f;
-        for (int64_t j = 0; j < period; ++j) amax = nanmax(amax, fabsf(load_dt(g, gdt, r * period + j)));
-        for (int64_t j = 0; j < period; ++j) {
-            float v = load_dt(g, gdt, r * period + j);
-            float x = (amax > 0.0f) ? v / amax : 0.0f;
-            float y = floorf((x + 1.0f) / bw);
-            int64_t b;
-            if (y != y) b = INT64_MIN; /* torch .to(long) of NaN on x86 */
-            else if (y >= 9.2e18f) b = INT64_MIN;
-            else if (y <= -9.2e18f) b = INT64_MIN;
-            else b = (int64_t)y;
-            if (b < 0) b = 0;
-            if (b > bins - 1) b = bins - 1;
-            counts[b] += 1;
+    /* integer counts per thread, added at the end: exact in any order */
+    int failed = 0;
+#pragma omp parallel if (n > (1 << 20)) reduction(| : failed)
+    {
+        int64_t* local = (int64_t*)calloc((size_t)bins, sizeof(int64_t));
+        if (!local) failed = 1;
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            if (!local) continue;
+            float amax = 0.0f;
+            for (int64_t j = 0; j < period; ++j) amax = nanmax(amax, fabsf(load_dt(g, gdt, r * period + j)));
+            for (int64_t j = 0; j < period; ++j) {
+                float v = load_dt(g, gdt, r * period + j);
+                float x = (amax > 0.0f) ? v / amax : 0.0f;
+                float y = floorf((x + 1.0f) / bw);
+                int64_t b;
+                if (y != y) b = INT64_MIN; /* torch .to(long) of NaN on x86 */
+                else if (y >= 9.2e18f) b = INT64_MIN;
+                else if (y <= -9.2e18f) b = INT64_MIN;
+                else b = (int64_t)y;
+                if (b < 0) b = 0;
+                if (b > bins - 1) b = bins - 1;
+                local[b] += 1;
+            }
+        }
+        if (local) {
+#pragma omp critical
+            for (int b = 0; b < bins; ++b) counts[b] += local[b];
+            free(local);
         }
     }
-    return 0;
+    return failed ? 2 : 0;
 }
 
 /* f32 accumulation of per-tensor counts in parameter order (gefen.py:331, 347, 365) */
@@ -498,6 +512,10 @@ int orc_period_scores(int gdt, const void* g, int64_t n, const int64_t* divs, in
                       int mode, double eps, double* scores) {
     double* L = (double*)malloc(sizeof(double) * (size_t)n);
     if (!L) return 2;
+    int invalid = 0;
+    /* every element and every divisor is computed on its own in a fixed order,
+     * so the threads change nothing in the results */
+#pragma omp parallel for schedule(static) reduction(| : invalid)
     for (int64_t i = 0; i < n; ++i) {
         float v = load_dt(g, gdt, i);
         double x;
@@ -505,22 +523,33 @@ int orc_period_scores(int gdt, const void* g, int64_t n, const int64_t* divs, in
         else if (mode == 2) { x = (double)v; x = x * x; }
         else x = (double)v;
         double y = x + eps;
-        if (y <= 0.0) { free(L); return 4; }
+        if (y <= 0.0) invalid = 1;
         L[i] = log(y);
     }
+    if (invalid) { free(L); return 4; }
     int64_t maxb = 0;
     for (int d = 0; d < nd; ++d) if (n / divs[d] > maxb) maxb = n / divs[d];
-    double* means = (double*)malloc(sizeof(double) * (size_t)(maxb > 0 ? maxb : 1));
-    for (int d = 0; d < nd; ++d) {
-        const int64_t p = divs[d];
-        const int64_t nb = n / p;
-        for (int64_t j = 0; j < nb; ++j) means[j] = np_sum(L + j * p, p) / (double)p;
-        for (int64_t j = 0; j + 1 < nb; ++j) means[j] = fabs(means[j + 1] - means[j]);
-        scores[d] = (nb >= 2) ? np_sum(means, nb - 1) / (double)(nb - 1) : NAN;
+    int rc = 0;
+#pragma omp parallel
+    {
+        double* means = (double*)malloc(sizeof(double) * (size_t)(maxb > 0 ? maxb : 1));
+        if (!means) {
+#pragma omp atomic write
+            rc = 2;
+        }
+#pragma omp for schedule(dynamic, 1)
+        for (int d = 0; d < nd; ++d) {
+            if (!means) continue;
+            const int64_t p = divs[d];
+            const int64_t nb = n / p;
+            for (int64_t j = 0; j < nb; ++j) means[j] = np_sum(L + j * p, p) / (double)p;
+            for (int64_t j = 0; j + 1 < nb; ++j) means[j] = fabs(means[j + 1] - means[j]);
+            scores[d] = (nb >= 2) ? np_sum(means, nb - 1) / (double)(nb - 1) : NAN;
+        }
+        free(means);
     }
-    free(means);
     free(L);
-    return 0;
+    return rc;
 }
 
 /* ------------------------------------------------------------------ GefenMuon

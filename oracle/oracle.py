@@ -337,7 +337,8 @@ class GefenOracle:
     """Gefen.step on the CPU path for a list of numpy parameters (gefen.py:1399-1420).
 
     params: list of dicts {"p": array (storage dtype, updated in place), "dtype": str,
-    "shape": tuple, "lr", "beta1", "beta2", "eps", "weight_decay"}.
+    "shape": tuple, "lr", "beta1", "beta2", "eps", "weight_decay"} and optionally
+    "sdtype" (state dtype, default "dtype").
     step(grads): one array or None per parameter.
     """
 
@@ -367,9 +368,11 @@ class GefenOracle:
         self.codebook = learn_codebook(gp)
 
     def _ensure_state(self, i: int, g: np.ndarray) -> TensorState:
+        """State dtype = the gradient dtype, or "sdtype" of the parameter (float32
+        under the reference's F_FP32 flag, gefen.py:53-69)."""
         if self.state[i] is None:
             dt = self.params[i]["dtype"]
-            self.state[i] = TensorState(g.size, self._predict(i, g), dt, dt)
+            self.state[i] = TensorState(g.size, self._predict(i, g), dt, self.params[i].get("sdtype", dt))
         return self.state[i]
 
     def step(self, grads: Sequence[Optional[np.ndarray]]) -> None:
@@ -386,7 +389,7 @@ class GefenOracle:
             p = prm["p"]
             gg = np.ascontiguousarray(g.reshape(-1))
             rc = lib().orc_gefen_step(
-                DT[dt], DT[dt], _ptr(p), _ptr(gg), _ptr(st.m_codebook), _ptr(st.m_magnitude),
+                DT[dt], DT[prm.get("sdtype", dt)], _ptr(p), _ptr(gg), _ptr(st.m_codebook), _ptr(st.m_magnitude),
                 _ptr(st.vmean), gg.size, st.period, st.pod or 0, _ptr(self.codebook),
                 self.codebook.size, b1, b2, prm["lr"], prm["eps"], prm["weight_decay"],
                 bc1, bc2, self.nthreads)

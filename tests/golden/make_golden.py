@@ -10,7 +10,8 @@ outputs are written (``tests/golden/*.npz`` and ``*.json``); nothing from the
 reference is copied.  The fixtures pin what no closed form can:
 
 * period choices and divisor scores of ``find_period_by_block_variance``
-  (numpy log + pairwise means; ``partitioning.py:119-167, 277-347``);
+  (numpy log + pairwise means; ``partitioning.py:119-167, 277-347``), also on
+  full-size tensors of the BASELINE configs (``periods_full.npz``);
 * the first-step codebook pipeline (torch histogram + exact DP;
   ``gefen.py:305-419``, ``quantization.py:206-258``);
 * 20-step trajectories of ``Gefen`` / ``GefenMuon`` on the CPU path
@@ -147,6 +148,51 @@ def make_periods(ref, out: Path) -> None:
     (out / "periods.json").write_text(json.dumps(manifest, indent=1))
 
 
+# Full-size tensors of the BASELINE configs, generated as bench.py generates
+# them (seed 2026, stream = the tensor's index in bench.py's parameter list):
+# (name, bench config, index, shape, dtype, rows of the gradient scale, e_lo, e_hi)
+PERIOD_FULL_CASES = [
+    ("gpt2_wte_f32", "gpt2", 0, (50257, 768), "f32", 50257, -14, -4),
+    ("llama8b_k_proj_bf16", "llama8b", 2, (1024, 4096), "bf16", 1, -17, -7),
+    ("llama8b_down_proj_bf16", "llama8b", 7, (4096, 14336), "bf16", 1, -17, -7),
+]
+
+
+def period_full_grad(case):
+    name, cfg, index, shape, dtype, rows, e_lo, e_hi = case
+    n = int(np.prod(shape))
+    return syn.round_to(syn.row_scaled_normal(2026, index, rows, n // rows, e_lo, e_hi), dtype).reshape(-1)
+
+
+def make_periods_full(ref, out: Path) -> None:
+    """Scores of every divisor and the chosen period of full-size config tensors
+    (partitioning.py:119-167, 277-347 on the CPU path of gefen.py:812-828).
+    Only scores and choices are stored; tests regenerate the inputs."""
+    _, _, ref_part, _ = ref
+    data = {}
+    manifest = []
+    for case in PERIOD_FULL_CASES:
+        name, cfg, index, shape, dtype = case[:5]
+        t0 = time.time()
+        g = period_full_grad(case)
+        grad = to_torch(g, dtype)
+        period_input = grad.detach().float().square().reshape(-1).cpu().numpy()
+        period = ref_part.find_period_by_block_variance(
+            period_input, print_results=False, parameter_name=name, parameter_shape=shape, backend="cpu",
+            input_is_squared=True, max_period=None)
+        n = period_input.size
+        divs = [p for p in ref_part.divisors(n) if n // p >= ref_part.DMNB]
+        scores = [float(ref_part.average_within_block_variance_cpu(period_input, None, p)) for p in divs]
+        data[name + "/divisors"] = np.array(divs, dtype=np.int64)
+        data[name + "/scores"] = np.array(scores, dtype=np.float64)
+        data[name + "/period"] = np.array(period, dtype=np.int64)
+        manifest.append({"name": name, "config": cfg, "index": index, "shape": list(shape), "dtype": dtype,
+                         "period": int(period), "checksum": syn.checksum(g), "seconds": round(time.time() - t0, 1)})
+        print("full period", name, period, flush=True)
+    np.savez_compressed(out / "periods_full.npz", **data)
+    (out / "periods_full.json").write_text(json.dumps(manifest, indent=1))
+
+
 # --------------------------------------------------------------------------- DP
 def make_dp(ref, out: Path) -> None:
     ref_gefen, _, ref_part, ref_quant = ref
@@ -226,9 +272,33 @@ TRAJ_CASES = {
     "muon_bf16": ("MUON_MINI", "bf16", "muon", 20, {}, (-10, -10)),
     "muon_f32": ("MUON_MINI", "f32", "muon", 10, {"nesterov": False, "weight_decay": 0.0, "lr": 2e-2}, (-10, -10)),
     "tiny_e2e_f32": ("TINY_E2E", "f32", "gefen_learn", 20, {"weight_decay": 0.1}, (-14, -4)),
+    "llamamini_bf16_f32state": ("LLAMA_MINI", "bf16", "gefen", 20, {"weight_decay": 0.01}, (-17, -7)),
 }
+# trajectories run with the reference's module flag F_FP32 = True (float32
+# optimizer state for reduced-precision parameters, gefen.py:53-69)
+F_FP32_CASES = {"llamamini_bf16_f32state"}
 SNAP_STEPS = (1, 2, 5, 10, 20)
 STATE_STEPS = (1, 2, 20)
+
+
+def _run_traj(opt, params, data, name, seed, steps, skip, dtype, e_lo, e_hi) -> None:
+    for step in range(1, steps + 1):
+        for i, (pname, t, mode) in enumerate(params):
+            if i in skip.get(step, ()):
+                t.grad = None
+                continue
+            g = ps.grad_for_step(seed, i, step, tuple(t.shape), dtype, mode, e_lo, e_hi)
+            t.grad = to_torch(g, dtype)
+        opt.step()
+        if step in SNAP_STEPS:
+            for i, (pname, t, _) in enumerate(params):
+                data["p{}/step{}".format(i, step)] = to_numpy(t)
+        if step in STATE_STEPS:
+            for i, (pname, t, _) in enumerate(params):
+                st = opt.state[t]
+                for key in ("m_codebook", "m_magnitude", "vmean"):
+                    if key in st:
+                        data["s{}/{}/step{}".format(i, key, step)] = to_numpy(st[key])
 
 
 def make_traj(ref, out: Path, name: str, codebook: np.ndarray) -> None:
@@ -261,23 +331,12 @@ def make_traj(ref, out: Path, name: str, codebook: np.ndarray) -> None:
     if kind != "gefen_learn":
         opt._gefen_codebook = torch.from_numpy(codebook.astype(np.float32)).clone()
     t0 = time.time()
-    for step in range(1, steps + 1):
-        for i, (pname, t, mode) in enumerate(params):
-            if i in skip.get(step, ()):
-                t.grad = None
-                continue
-            g = ps.grad_for_step(seed, i, step, tuple(t.shape), dtype, mode, e_lo, e_hi)
-            t.grad = to_torch(g, dtype)
-        opt.step()
-        if step in SNAP_STEPS:
-            for i, (pname, t, _) in enumerate(params):
-                data["p{}/step{}".format(i, step)] = to_numpy(t)
-        if step in STATE_STEPS:
-            for i, (pname, t, _) in enumerate(params):
-                st = opt.state[t]
-                for key in ("m_codebook", "m_magnitude", "vmean"):
-                    if key in st:
-                        data["s{}/{}/step{}".format(i, key, step)] = to_numpy(st[key])
+    if name in F_FP32_CASES:
+        ref_gefen.F_FP32 = True
+    try:
+        _run_traj(opt, params, data, name, seed, steps, skip, dtype, e_lo, e_hi)
+    finally:
+        ref_gefen.F_FP32 = False
     periods = [int(opt.state[t]["automatic_period"]) for _, t, _ in params]
     data["periods"] = np.array(periods, dtype=np.int64)
     data["codebook_out"] = opt._gefen_codebook.numpy().astype(np.float32)
@@ -295,6 +354,7 @@ def make_traj(ref, out: Path, name: str, codebook: np.ndarray) -> None:
     (out / "traj_{}.json".format(name)).write_text(json.dumps(
         {"name": name, "param_set": set_name, "dtype": dtype, "kind": kind, "steps": steps,
          "kwargs": kwargs, "e_range": [e_lo, e_hi], "seed": seed, "skip": {str(k): sorted(v) for k, v in skip.items()},
+         "f_fp32": name in F_FP32_CASES,
          "periods": periods, "seconds": round(time.time() - t0, 1), "state_dict": layout}, indent=1, default=str))
     print("traj", name, "periods", periods, "in", round(time.time() - t0, 1), "s", flush=True)
 
@@ -439,6 +499,8 @@ def main() -> None:
     out = HERE
     if args.only in (None, "periods"):
         make_periods(ref, out)
+    if args.only in (None, "periods_full"):
+        make_periods_full(ref, out)
     if args.only in (None, "dp"):
         make_dp(ref, out)
     if args.only in (None, "ns"):

@@ -40,10 +40,15 @@ def _build_gefen(meta, tensors, params):
 
 
 @pytest.mark.parametrize("name", [n for n in tu.TRAJ_NAMES if not n.startswith("muon")])
-def test_gefen_matches_reference_trajectory(name):
+def test_gefen_matches_reference_trajectory(name, monkeypatch):
+    from gefen_amd import gefen as gefen_mod
+
     print("trajectory", name, flush=True)
     data, meta, params, skip = tu.build(name)
     dtype = meta["dtype"]
+    sdtype = "f32" if meta.get("f_fp32") else dtype
+    if meta.get("f_fp32"):
+        monkeypatch.setattr(gefen_mod, "F_FP32", True)
     tensors = _params(params, dtype)
     opt = _build_gefen(meta, tensors, params)
     if meta["kind"] != "gefen_learn":
@@ -66,9 +71,9 @@ def test_gefen_matches_reference_trajectory(name):
                 np.testing.assert_array_equal(gu.to_np(st["m_magnitude"]).reshape(-1),
                                               tu.bits(data[key]).reshape(-1), err_msg=key)
                 key = "s{}/vmean/step{}".format(i, step)
-                vg = orc.to_f32(gu.to_np(st["vmean"]).reshape(-1), dtype)
-                vr = orc.to_f32(tu.bits(data[key]).reshape(-1), dtype)
-                if dtype == "f32":
+                vg = orc.to_f32(gu.to_np(st["vmean"]).reshape(-1), sdtype)
+                vr = orc.to_f32(tu.bits(data[key]).reshape(-1), sdtype)
+                if sdtype == "f32":
                     np.testing.assert_allclose(vg, vr, rtol=4e-6, atol=0, err_msg=key)
                 else:
                     assert tu.ulp_distance_bf16(gu.to_np(st["vmean"]).reshape(-1),

@@ -92,9 +92,10 @@ def test_gefen_trajectory_matches_reference(name):
                 key = "s{}/m_magnitude/step{}".format(i, step)
                 np.testing.assert_array_equal(st.m_magnitude, tu.bits(data[key]).reshape(-1), err_msg=key)
                 key = "s{}/vmean/step{}".format(i, step)
-                vref = orc.to_f32(tu.bits(data[key]).reshape(-1), prm["dtype"])
-                vgot = orc.to_f32(st.vmean, prm["dtype"])
-                if prm["dtype"] == "f32":
+                sdt = prm.get("sdtype", prm["dtype"])
+                vref = orc.to_f32(tu.bits(data[key]).reshape(-1), sdt)
+                vgot = orc.to_f32(st.vmean, sdt)
+                if sdt == "f32":
                     np.testing.assert_allclose(vgot, vref, rtol=2e-6, atol=0, err_msg=key)
                 else:
                     assert tu.ulp_distance_bf16(st.vmean, tu.bits(data[key]).reshape(-1)).max() <= 1, key
@@ -271,3 +272,22 @@ def test_block_variance_oracle_matches_closed_form():
     assert out[1] == 50 and out[2] == 0
     out = orc.block_variance(-np.ones(8, np.float32), "f32", 4, True, True)
     assert out[2] == 2 and out[1] == 0
+
+
+def test_full_size_period_fixture_k_proj():
+    """The oracle on a full-size config tensor (Llama-3-8B k_proj, 4.2M bf16
+    elements, regenerated from its seed) against the reference's scores; the two
+    larger tensors of periods_full.npz are checked on the GPU box, where their
+    inputs come from the device generator."""
+    from gefen_amd import synthetic as syn
+    import make_golden as mg
+
+    data, meta = load("periods_full")
+    case = next(c for c in mg.PERIOD_FULL_CASES if c[0] == "llama8b_k_proj_bf16")
+    m = next(x for x in meta if x["name"] == case[0])
+    g = mg.period_full_grad(case)
+    assert syn.checksum(g) == m["checksum"]
+    divs = data[case[0] + "/divisors"].tolist()
+    np.testing.assert_allclose(orc.period_scores(g, "bf16", divs, mode=1), data[case[0] + "/scores"], rtol=1e-13,
+                               atol=0)
+    assert orc.find_period(g, "bf16") == m["period"]

@@ -13,7 +13,7 @@ import param_sets as ps
 from golden_util import load
 
 TRAJ_NAMES = ["gpt2mini_f32", "llamamini_bf16", "fp16mini", "groups_f32", "muon_bf16", "muon_f32",
-              "tiny_e2e_f32"]
+              "tiny_e2e_f32", "llamamini_bf16_f32state"]
 
 
 def group_options(meta, n_params):
@@ -50,6 +50,8 @@ def build(name):
     opts = group_options(meta, len(params))
     for prm, o in zip(params, opts):
         prm.update(o)
+        if meta.get("f_fp32"):
+            prm["sdtype"] = "f32"
     skip = {int(k): set(v) for k, v in meta["skip"].items()}
     return data, meta, params, skip
 
