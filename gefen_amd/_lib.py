@@ -41,7 +41,9 @@ SIGNATURES = {
     "gefen_step_tasks": (I32, [P, I32, P, P]),
     "gefen_step_tasks_noalloc": (I32, [P, I32, P, P]),
     "gefen_muon_tasks": (I32, [P, I32, P, P]),
+    "gefen_muon_tasks_sumsq": (I32, [P, I32, P, P, P]),
     "gefen_ns_prepare": (I32, [P, P, I32, I32, I32, DBL, P]),
+    "gefen_ns_prepare_sumsq": (I32, [P, P, I32, I32, I32, DBL, P, P, P]),
     "gefen_muon_apply_tasks": (I32, [P, I32, P]),
     "gefen_exact_histogram": (I32, [P, I32, I64, I64, P, I32, P]),
     "gefen_accumulate_counts": (I32, [P, P, I32, P]),

@@ -71,17 +71,51 @@ __global__ void k_norm(const float* __restrict__ partial, int nblk, int batch, f
     div[g] = (nrm < eps_bf16) ? eps_bf16 : nrm;
 }
 
-// x[g] = bf16(x[g] / div[g]) in place, xt[g] = x[g]^T; one 64 x 64 tile per block
+// clamp(min=eps) of a bf16 tensor compares with eps rounded to bf16
+inline float eps_to_bf16(double eps) {
+    const float f = (float)eps;
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float r;
+    memcpy(&r, &u, 4);
+    return r;
+}
+
+// Divisor of matrix g from its float64 sum of squares (gefen_ns_prepare_sumsq):
+// max(bf16(sqrt(sum)), bf16(eps)), as k_norm forms it.
+__device__ __forceinline__ float divisor_from_sumsq(double s, float eps_bf16) {
+    const float nrm = round_to<bf16_t>((float)sqrt(s));
+    return (nrm < eps_bf16) ? eps_bf16 : nrm;
+}
+
+// x[g] = bf16(x[g] / d_g) in place, xt[g] = x[g]^T; one 64 x 64 tile per block.
+// d_g = div[g], or from the sum of the GEFEN_SUMSQ_SLOTS partial sums of
+// task index[g] (or g) when sumsq is given.  The
+// quotient is the float64 product with 1 / d_g rounded to float (the IEEE
+// quotient: see div_by_block), then rounded to bf16 as torch's bf16 div_ does.
 constexpr int kTile = 64;
 __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ x, uint16_t* __restrict__ xt,
-                                                         int rows, int cols, const float* __restrict__ div) {
+                                                         int rows, int cols, const float* __restrict__ div,
+                                                         const double* __restrict__ sumsq,
+                                                         const int32_t* __restrict__ index, float eps_bf16) {
     __shared__ uint16_t tile[kTile][kTile + 2];
     const int g = blockIdx.z;
     const int r0 = blockIdx.y * kTile, c0 = blockIdx.x * kTile;
     const int64_t per = (int64_t)rows * cols;
     uint16_t* src = x + (int64_t)g * per;
     uint16_t* dst = xt + (int64_t)g * per;
-    const float d = div[g];
+    float d;
+    if (sumsq) {
+        const double* slots = sumsq + (size_t)(index ? index[g] : g) * GEFEN_SUMSQ_STRIDE;
+        double s = 0.0;
+        for (int i = 0; i < GEFEN_SUMSQ_SLOTS; ++i) s += slots[16 * i];
+        d = divisor_from_sumsq(s, eps_bf16);
+    } else {
+        d = div[g];
+    }
+    const double rd = 1.0 / (double)d;
     const int t = threadIdx.x;
     {
         const int r = t >> 2, cc = (t & 3) * 16;  // 16 elements of row r
@@ -91,8 +125,8 @@ __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ 
             u32x4 v = *reinterpret_cast<const u32x4*>(p + 8 * h);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const float lo = __uint_as_float(v[c] << 16) / d;
-                const float hi = __uint_as_float(v[c] & 0xffff0000u) / d;
+                const float lo = div_by_block(__uint_as_float(v[c] << 16), rd);
+                const float hi = div_by_block(__uint_as_float(v[c] & 0xffff0000u), rd);
                 const uint32_t blo = from_f32<bf16_t>(lo).bits, bhi = from_f32<bf16_t>(hi).bits;
                 v[c] = blo | (bhi << 16);
                 tile[r][cc + 8 * h + 2 * c] = (uint16_t)blo;
@@ -197,16 +231,7 @@ extern "C" int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols
     if (e != hipSuccess) return hip_status(e, "hipMallocAsync(norm partials)");
     float* partial = static_cast<float*>(ws);
     float* div = partial + (size_t)batch * nblk;
-    const float eps_bf16 = [&] {  // clamp(min=eps) of a bf16 tensor compares with eps rounded to bf16
-        const float f = (float)eps;
-        uint32_t u;
-        memcpy(&u, &f, 4);
-        u += 0x7fffu + ((u >> 16) & 1u);
-        u &= 0xffff0000u;
-        float r;
-        memcpy(&r, &u, 4);
-        return r;
-    }();
+    const float eps_bf16 = muon::eps_to_bf16(eps);
     auto* X = static_cast<uint16_t*>(x);
     hipLaunchKernelGGL(muon::k_sumsq, dim3(nblk, batch), dim3(muon::kNormThreads), 0, st, X, per, nblk, partial);
     int rc = launch_status("gefen_ns_prepare (norm)");
@@ -216,11 +241,27 @@ extern "C" int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols
     }
     if (rc == GEFEN_OK) {
         hipLaunchKernelGGL(muon::k_scale_transpose, dim3(cols / muon::kTile, rows / muon::kTile, batch), dim3(256), 0,
-                           st, X, static_cast<uint16_t*>(xt), rows, cols, div);
+                           st, X, static_cast<uint16_t*>(xt), rows, cols, div, nullptr, nullptr, 0.0f);
         rc = launch_status("gefen_ns_prepare (scale)");
     }
     (void)hipFreeAsync(ws, st);
     return rc;
+}
+
+extern "C" int gefen_ns_prepare_sumsq(void* x, void* xt, int batch, int rows, int cols, double eps,
+                                     const double* sumsq, const int32_t* index, gefen_stream_t stream) {
+    if (batch < 0 || rows < 0 || cols < 0) return fail_inval("negative size");
+    if (batch == 0 || rows == 0 || cols == 0) return GEFEN_OK;
+    if (!x || !xt || !sumsq) return fail_inval("null pointer");
+    if (rows % muon::kTile || cols % muon::kTile)
+        return fail_inval("gefen_ns_prepare needs rows and cols that are multiples of 64 (got %d, %d)", rows, cols);
+    if (!aligned(x, 16) || !aligned(xt, 16)) return fail_inval("gefen_ns_prepare needs 16-byte aligned buffers");
+    if (batch > 65535) return fail_inval("batch too large");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(muon::k_scale_transpose, dim3(cols / muon::kTile, rows / muon::kTile, batch), dim3(256), 0, st,
+                       static_cast<uint16_t*>(x), static_cast<uint16_t*>(xt), rows, cols, nullptr, sumsq, index,
+                       muon::eps_to_bf16(eps));
+    return launch_status("gefen_ns_prepare_sumsq");
 }
 
 extern "C" int gefen_muon_apply_tasks(const gefen_muon_apply_task* tasks, int ntasks, gefen_stream_t stream) {

@@ -576,6 +576,7 @@ struct MuonTask {
     float tiny;    // finfo(D).tiny rounded to S
     int32_t nesterov;
     int32_t nwg;
+    double* sumsq;  // if set: GEFEN_SUMSQ_SLOTS accumulators (16 doubles apart) of the sum of squares of the output
 };
 
 struct MuonBatch {
@@ -586,6 +587,22 @@ struct MuonBatch {
     const CodebookTables* tables;
 };
 static_assert(sizeof(MuonBatch) <= 4000, "kernel arguments are limited to 4 KB");
+
+// Workgroup sum of the lanes' sums of squares (kThreads lanes), added to slot
+// `key mod GEFEN_SUMSQ_SLOTS` of a task's accumulators (one 128-byte line each):
+// one float64 atomic per workgroup, spread over separate lines.
+__device__ __forceinline__ void add_sumsq(float v, double* sumsq, int64_t key) {
+    __shared__ float red[kThreads / 64];
+    v = group_sum(v, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) t = t + red[w];
+        atomicAdd(sumsq + 16 * (key & (GEFEN_SUMSQ_SLOTS - 1)), (double)t);
+    }
+}
 
 // Nesterov blend of gefen_muon.py:312-316 on a = D(q * momentum): add_(g, alpha)
 template <typename D>
@@ -626,6 +643,7 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     const int64_t lw = blockIdx.x - B.wg_begin[ti];
     float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
     float* otab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
+    float wsq = 0.0f;  // this lane's sum of squares of the outputs it wrote
 
     for (int it = 0; it < kMuonIter; ++it) {
         const int64_t unit = (lw * kMuonIter + it) * 4 + wave;
@@ -699,10 +717,12 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
+        float sq = 0.0f;  // sum of squares of the outputs this lane writes
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             Vec<uint8_t, W> io;
             Vec<D, W> oo;
+            float sqj = 0.0f;
 #pragma unroll
             for (int w = 0; w < W; ++w) {
                 int k;
@@ -716,15 +736,20 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
                 io.v[w] = (uint8_t)k;
                 const float a = TAB ? otab[k] : out_base(k);
                 oo.v[w] = from_f32<D>(muon_blend<D>(a, to_f32(gv[j].v[w]), T));
+                const float o = to_f32(oo.v[w]);
+                sqj = __builtin_fmaf(o, o, sqj);
             }
             const int v = lir + j * lpr;
             if (active && v < T.nvec) {
                 const uint32_t e = base + (uint32_t)(v * W);
                 sstore<uint8_t, W>(idx, e, io);
                 sstore<D, W>(out, e, oo);
+                sq += sqj;
             }
         }
+        wsq += sq;
     }
+    if (T.sumsq) add_sumsq(wsq, T.sumsq, lw);  // uniform: one task per workgroup
 }
 
 template <typename D, typename S>
@@ -759,6 +784,7 @@ __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
     const float clamped = (ms < T.tiny) ? T.tiny : ms;
     __syncthreads();
     if (threadIdx.x == 0) mag[row] = mag_s;
+    float sq = 0.0f;
     for (int64_t j = threadIdx.x; j < T.rowlen; j += kThreads) {
         const float gf = to_f32(g[base + j]);
         const float m0 = round_to<D>(L.cbd[idx[base + j]] * mold);
@@ -768,8 +794,12 @@ __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
         const int k = nearest_fast(x, L.thr, L.bucket, K);
         idx[base + j] = (uint8_t)k;
         const float q = round_to<D>(L.cbd[k] * ms);
-        out[base + j] = from_f32<D>(muon_out<D, S>(q, gf, T));
+        const D o = from_f32<D>(muon_out<D, S>(q, gf, T));
+        out[base + j] = o;
+        const float of = to_f32(o);
+        sq = __builtin_fmaf(of, of, sq);
     }
+    if (T.sumsq) add_sumsq(sq, T.sumsq, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -950,6 +980,12 @@ __global__ __launch_bounds__(256) void k_build_root(float* __restrict__ root, St
         const int m = i < 256 ? 128 + (i & 127) : i - 256;
         root[i] = __builtin_ldexpf(sqrtf((float)m * (par ? 2.0f : 1.0f)) / T.sqrt_bc2, -67);
     }
+}
+
+// x[0, n) = 0 (the accumulator slots of gefen_muon_tasks_sumsq)
+__global__ __launch_bounds__(256) void k_fill_f64(double* __restrict__ x, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = 0.0;
 }
 
 // Stepsize table of a period-one tensor with an f16 state: lut[b] is the
@@ -1777,8 +1813,8 @@ int flush_muon(std::vector<PendingMuon>& pend, const CodebookTables* tables, hip
 }  // namespace
 }  // namespace gefen
 
-extern "C" int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* tables,
-                                gefen_stream_t stream) {
+static int muon_tasks_common(const gefen_muon_task* tasks, int ntasks, const void* tables, double* sumsq,
+                             gefen_stream_t stream) {
     if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
     if (!tables) return fail_inval("null codebook tables");
     std::vector<PendingMuon> pend;
@@ -1787,9 +1823,28 @@ extern "C" int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const 
         PendingMuon pm;
         int rc = make_muon_task(tasks[i], pm);
         if (rc) return rc;
+        pm.task.sumsq = sumsq ? sumsq + (size_t)i * GEFEN_SUMSQ_STRIDE : nullptr;
         pend.push_back(pm);
     }
-    return flush_muon(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (sumsq && ntasks > 0) {  // a fill kernel, not a memset node (callers may capture this)
+        const int n = ntasks * GEFEN_SUMSQ_STRIDE;
+        hipLaunchKernelGGL(k_fill_f64, dim3((n + 255) / 256), dim3(256), 0, st, sumsq, n);
+        int rc = launch_status("gefen muon sumsq init");
+        if (rc) return rc;
+    }
+    return flush_muon(pend, static_cast<const CodebookTables*>(tables), st);
+}
+
+extern "C" int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* tables,
+                                gefen_stream_t stream) {
+    return muon_tasks_common(tasks, ntasks, tables, nullptr, stream);
+}
+
+extern "C" int gefen_muon_tasks_sumsq(const gefen_muon_task* tasks, int ntasks, const void* tables, double* sumsq,
+                                      gefen_stream_t stream) {
+    if (!sumsq && ntasks > 0) return fail_inval("null sumsq");
+    return muon_tasks_common(tasks, ntasks, tables, sumsq, stream);
 }
 
 extern "C" int gefen_automatic_muon_momentum(const void* grad, int grad_dtype, uint8_t* m_sign,

@@ -22,6 +22,7 @@ from gefen_amd.gefen import (Gefen, _DTYPE_CODE, _distinct, _gefen_host, _plan_c
                              _decay_from_lr_tensor, _tensor_lr_with_decay, automatic_partition_view)
 
 EPS = 1e-7
+_SUMSQ_STRIDE = 128  # GEFEN_SUMSQ_STRIDE (include/gefen_hip.h): sum-of-squares entries per momentum task
 DEFAULT_A = 3.4445
 DEFAULT_B = -4.7750
 DEFAULT_C = 2.0315
@@ -209,10 +210,15 @@ class GefenMuon(Gefen):
             t["nesterov"] = 1 if group["nesterov"] else 0
         dev = items[0][3].device
         lib = _lib.load()
+        # the sums of squares of the written blends of bf16 stacks, for the
+        # Newton-Schulz normalisation (gathered by the momentum kernels)
+        sumsq = torch.empty(len(items) * _SUMSQ_STRIDE, dtype=torch.float64, device=dev)
+        sum_index = {key: torch.tensor(idx, dtype=torch.int32, device=dev)
+                     for key, idx in stacks.items() if key[2] == torch.bfloat16}
         with torch.cuda.device(dev):
-            rc = lib.gefen_muon_tasks(tasks.ctypes.data, len(items), tables.data_ptr(),
-                                      torch.cuda.current_stream(dev).cuda_stream)
-        _lib.check(rc, "gefen_muon_tasks")
+            rc = lib.gefen_muon_tasks_sumsq(tasks.ctypes.data, len(items), tables.data_ptr(), sumsq.data_ptr(),
+                                            torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(rc, "gefen_muon_tasks_sumsq")
         updates = {}
         works = {}
         if stacks:
@@ -223,7 +229,9 @@ class GefenMuon(Gefen):
                 _check_ns_args(coeffs, steps)
                 x = bufs[key] if key[2] == torch.bfloat16 else bufs[key].bfloat16()
                 works[key] = {}
-                res = newton_schulz_batched(x, coeffs, steps, eps, work=works[key])
+                si = sum_index.get(key)
+                res = newton_schulz_batched(x, coeffs, steps, eps, work=works[key],
+                                            sumsq=sumsq if si is not None else None, index=si)
                 for slot, i in enumerate(idx):
                     updates[i] = res[slot]
         apply = np.zeros(len(items), dtype=_lib.MUON_APPLY_TASK)
@@ -271,8 +279,8 @@ class GefenMuon(Gefen):
         plain = (not copy_back and len(where) == len(items)
                  and all(local_p is p and grad is p.grad and grad.is_contiguous() for (_, p, local_p, grad) in items))
         if plain:
-            self._plan = _MuonPlan(self, items, tasks, apply, [(key, idx, bufs[key], works[key])
-                                                                 for key, idx in stacks.items()], dev)
+            self._plan = _MuonPlan(self, items, tasks, apply, [(key, idx, bufs[key], works[key], sum_index.get(key))
+                                                                 for key, idx in stacks.items()], dev, sumsq)
         del keep
 
     @torch.no_grad()
@@ -299,7 +307,7 @@ class _MuonPlan:
     refreshes gradient addresses, step counts, lr, weight decay, momentum and
     Nesterov, and returns True.  Otherwise it changes nothing and returns False."""
 
-    def __init__(self, opt, items, mtasks, apply, stacks, device):
+    def __init__(self, opt, items, mtasks, apply, stacks, device, sumsq):
         self.params = [it[1] for it in items]
         self.pptr = [it[1].data_ptr() for it in items]
         self.numel = [it[3].numel() for it in items]
@@ -318,6 +326,7 @@ class _MuonPlan:
         self.mtasks = mtasks.copy()
         self.apply = apply.copy()
         self.stacks = stacks
+        self.sumsq = sumsq
         self.settings = self._settings()
         self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.state_keys)
         self.steps = np.zeros(len(items), dtype=np.int64)
@@ -368,16 +377,17 @@ class _MuonPlan:
         tables = opt._codebook_tables()
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            _lib.check(lib.gefen_muon_tasks(self.mtasks.ctypes.data, len(self.mtasks), tables.data_ptr(), stream),
-                       "gefen_muon_tasks")
+            _lib.check(lib.gefen_muon_tasks_sumsq(self.mtasks.ctypes.data, len(self.mtasks), tables.data_ptr(),
+                                                  self.sumsq.data_ptr(), stream), "gefen_muon_tasks_sumsq")
             # newton_schulz_batched may return its input (a bf16 copy of a non-bf16
             # stack, with an even or zero step count): every input and result stays
             # referenced here until the launch that reads them is enqueued
             keep = []
-            for key, idx, buf, work in self.stacks:
+            for key, idx, buf, work, sum_index in self.stacks:
                 coeffs, steps, eps = key[3], key[4], key[5]
                 x = buf if key[2] == torch.bfloat16 else buf.bfloat16()
-                res = newton_schulz_batched(x, coeffs, steps, eps, work=work)
+                res = newton_schulz_batched(x, coeffs, steps, eps, work=work,
+                                            sumsq=self.sumsq if sum_index is not None else None, index=sum_index)
                 keep.append((x, res))
                 slot_bytes = res[0].numel() * res.element_size()
                 self.apply["update"][idx] = res.data_ptr() + np.arange(len(idx), dtype=np.uint64) * slot_bytes

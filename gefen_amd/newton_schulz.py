@@ -93,13 +93,17 @@ def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: 
 
 
 def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], steps: int,
-                          eps: float, work: Optional[dict] = None) -> torch.Tensor:
+                          eps: float, work: Optional[dict] = None, sumsq: Optional[torch.Tensor] = None,
+                          index: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Newton-Schulz of every matrix of a [G, rows, cols] bf16 stack, in place of
     x's values (x is normalised in place); returns the [G, rows, cols] result.
 
     work: a dict that keeps the intermediate buffers between calls with the same
     stack (allocated on first use); the result is then the same buffer on every
-    call with the same number of steps."""
+    call with the same number of steps.
+    sumsq, index: the matrices' sums of squares, already gathered (float64 device
+    tensor; matrix g's is sumsq[index[g]], int32 device index, or sumsq[g]), so
+    the normalisation does not read the stack twice."""
     a, b, c = coeffs
     g, rows, cols = x.shape
     transposed = rows > cols
@@ -117,8 +121,14 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
     other = buf("other", (g, cols, rows))
     lib = _lib.load()
     with torch.cuda.device(x.device):
-        _lib.check(lib.gefen_ns_prepare(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps),
-                                        torch.cuda.current_stream(x.device).cuda_stream), "gefen_ns_prepare")
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        if sumsq is not None:
+            _lib.check(lib.gefen_ns_prepare_sumsq(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps),
+                                                  sumsq.data_ptr(), index.data_ptr() if index is not None else None,
+                                                  stream), "gefen_ns_prepare_sumsq")
+        else:
+            _lib.check(lib.gefen_ns_prepare(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps), stream),
+                       "gefen_ns_prepare")
     x, xt = (other, x) if transposed else (x, other)
     m, n = x.shape[1], x.shape[2]
     gram = buf("gram", (g, m, m))

@@ -164,12 +164,34 @@ typedef struct gefen_muon_task {
 int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* tables,
                      gefen_stream_t stream);
 
+/* gefen_muon_tasks, and the sum of squares of task i's output values: the
+ * input of the Frobenius norm that gefen_ns_prepare_sumsq divides by, gathered
+ * while the output is written instead of by another pass over it.  sumsq holds
+ * GEFEN_SUMSQ_STRIDE float64 entries per task (device, ntasks * GEFEN_SUMSQ_STRIDE
+ * entries, set to zero first), of which GEFEN_SUMSQ_SLOTS partial sums, one per
+ * 128-byte line: task i's sum is the sum over s of
+ * sumsq[i * GEFEN_SUMSQ_STRIDE + 16 * s].  Each workgroup adds its float32 sum
+ * to one slot with a float64 atomic, so the last bits may vary between runs;
+ * the norm is rounded to bf16 from them. */
+#define GEFEN_SUMSQ_SLOTS 8
+#define GEFEN_SUMSQ_STRIDE (16 * GEFEN_SUMSQ_SLOTS)
+int gefen_muon_tasks_sumsq(const gefen_muon_task* tasks, int ntasks, const void* tables, double* sumsq,
+                           gefen_stream_t stream);
+
 /* Replaces the bf16 normalisation before Newton-Schulz (gefen_muon.py:37,
  * ortho_grad.div_(ortho_grad.norm().clamp(min=eps)), done by torch in the
  * reference) for a stack of `batch` bf16 matrices [rows, cols] (contiguous):
  * x[g] = bf16(x[g] / max(bf16(||x[g]||), bf16(eps))) in place, and
  * xt[g] = x[g]^T [cols, rows].  rows and cols multiples of 64. */
 int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols, double eps, gefen_stream_t stream);
+
+/* gefen_ns_prepare with each matrix's sum of squares given as the partial sums
+ * gefen_muon_tasks_sumsq leaves for the bf16 outputs it wrote into the stack:
+ * matrix g's norm is the square root of the sum over s of
+ * sumsq[t * GEFEN_SUMSQ_STRIDE + 16 * s], t = index[g] (t = g when index is
+ * NULL; both device arrays). */
+int gefen_ns_prepare_sumsq(void* x, void* xt, int batch, int rows, int cols, double eps, const double* sumsq,
+                           const int32_t* index, gefen_stream_t stream);
 
 /* Replaces the parameter update of gefen_muon.py:325-329 (p.mul_(1 - lr*wd);
  * p.add_(update, alpha=-lr_adj)) with the reference's CPU rounding: reduced

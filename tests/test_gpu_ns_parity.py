@@ -182,3 +182,51 @@ def test_muon_steps_match_reference_blend_update_and_newton_schulz(name, monkeyp
             ref = orc.to_f32(ns_out, "bf16").reshape(prm["shape"]).astype(np.float64)
             rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
             assert rel <= 0.02, (key, rel)
+
+
+def test_momentum_sums_of_squares_feed_the_same_normalisation():
+    """gefen_muon_tasks_sumsq leaves each task's sum of squares of the outputs it
+    wrote (float32 sums per lane and wave, added in float64: within 1e-5 of a
+    float64 sum of the same values; the norm is rounded to bf16 from it), and
+    gefen_ns_prepare_sumsq with those sums normalises and transposes the stack
+    bit-identically to gefen_ns_prepare, which computes the norms itself."""
+    from gefen_amd import _lib
+    from gefen_amd import synthetic as syn
+
+    lib = _lib.load()
+    data, _ = load("exact_dp")
+    cb = torch.from_numpy(data["hist_k256_forced/codebook"]).to("cuda:0")
+    tables = torch.empty(int(lib.gefen_codebook_tables_size()), dtype=torch.uint8, device="cuda:0")
+    _lib.check(lib.gefen_prepare_codebook(cb.data_ptr(), cb.numel(), tables.data_ptr(), gu.stream()))
+    G, rows, cols = 5, 256, 512
+    stack = torch.empty(G, rows, cols, dtype=torch.bfloat16, device="cuda:0")
+    grads = [torch.empty(rows * cols, dtype=torch.bfloat16, device="cuda:0") for _ in range(G)]
+    states = []
+    tasks = np.zeros(G, dtype=_lib.MUON_TASK)
+    for i, g in enumerate(grads):
+        syn.fill_device(g, 77, i, syn.KIND_ROW_SCALED, cols=cols, e_lo=-12, e_hi=-8)
+        block = (512, 256, 128, 1024, 2048)[i]  # magnitude blocks of several lengths
+        idx = torch.zeros(rows * cols, dtype=torch.uint8, device="cuda:0")
+        mag = torch.zeros(rows * cols // block, dtype=torch.bfloat16, device="cuda:0")
+        states.append((idx, mag))
+        t = tasks[i]
+        t["grad"], t["m_codebook"], t["m_magnitude"] = g.data_ptr(), idx.data_ptr(), mag.data_ptr()
+        t["out"], t["numel"], t["block"] = stack[i].data_ptr(), rows * cols, block
+        t["grad_dtype"] = t["state_dtype"] = gu.CODE["bf16"]
+        t["momentum"], t["nesterov"] = 0.95, 1
+    sumsq = torch.empty(G * 128, dtype=torch.float64, device="cuda:0")  # GEFEN_SUMSQ_STRIDE per task
+    for _ in range(2):  # twice: the sums restart from zero on every call
+        _lib.check(lib.gefen_muon_tasks_sumsq(tasks.ctypes.data, G, tables.data_ptr(), sumsq.data_ptr(),
+                                              gu.stream()))
+    ref = (stack.double() ** 2).sum(dim=(1, 2))
+    assert torch.allclose(sumsq.view(G, 8, 16)[:, :, 0].sum(1), ref, rtol=1e-5, atol=0), (sumsq, ref)
+    x1, x2 = stack.clone(), stack.clone()
+    t1 = torch.empty(G, cols, rows, dtype=torch.bfloat16, device="cuda:0")
+    t2 = torch.empty_like(t1)
+    order = torch.tensor([4, 3, 2, 1, 0], dtype=torch.int32, device="cuda:0")
+    x2 = x2.flip(0).contiguous()  # matrix g of x2 is task 4 - g: found through the index
+    _lib.check(lib.gefen_ns_prepare(x1.data_ptr(), t1.data_ptr(), G, rows, cols, 1e-7, gu.stream()))
+    _lib.check(lib.gefen_ns_prepare_sumsq(x2.data_ptr(), t2.data_ptr(), G, rows, cols, 1e-7, sumsq.data_ptr(),
+                                          order.data_ptr(), gu.stream()))
+    assert torch.equal(x1.view(torch.int16), x2.flip(0).view(torch.int16))
+    assert torch.equal(t1.view(torch.int16), t2.flip(0).view(torch.int16))
