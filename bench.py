@@ -7,7 +7,9 @@ Llama-3-8B-shaped parameter set (291 tensors, 8.03e9 bf16 parameters, bf16
 gradients, untied embed / lm_head).  Inputs are synthetic (integer-exact
 generator, gefen_amd/synthetic.py) and created in HBM before timing:
 parameters ~ N(0, 0.02), gradients ~ N(0, 1) times a per-tensor dyadic
-log-uniform scale in [2^-17, 2^-7] (~[1e-5, 1e-2]).
+log-uniform scale in [2^-17, 2^-7] (~[7.6e-6, 7.8e-3]; BASELINE.json names
+[1e-5, 1e-2]).  Before every step after the first, new gradient values are
+written into the same gradient buffers (outside the timed region).
 
 * value / ms_per_step: median wall time of one ``optimizer.step()`` over the
   timed steps (synchronised per step), steady state (steps after the first).
@@ -176,6 +178,8 @@ def bench_kernels(args, dev):
            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                         "kernel": "period scores: one read of the 256 MB tensor for all divisors"}}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_kernels(g.cpu().numpy(), divs)
     print(json.dumps(out), flush=True)
 
 
@@ -232,15 +236,33 @@ def step_bytes(opt, params):
     return total
 
 
+STEP_KERNEL_SOURCES = ("gefen_amd/csrc/step.hip", "gefen_amd/csrc/common.h")
+
+
+def step_kernel_sources_sha256():
+    """sha256 of the step kernels' sources: a traffic record applies only to the
+    kernels it was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in STEP_KERNEL_SOURCES:
+        h.update(rel.encode())
+        h.update((REPO / rel).read_bytes())
+    return h.hexdigest()
+
+
 def measured_traffic(cfg, nbytes):
     """HBM bytes per step of the k_gefen_step launches from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known
-    size), when they were taken on this workload with the same algorithmic bytes."""
+    size), when they were taken on this workload with the same algorithmic bytes
+    and the same kernel sources (else None: a stale record is never reported)."""
     path = REPO / "profiles" / "k_gefen_step_llama8b_traffic.json"
     if not path.exists():
         return None
     rec = json.loads(path.read_text())
     if rec.get("workload") != cfg["workload"] or rec.get("algorithmic_bytes_per_step") != int(nbytes):
+        return None
+    if rec.get("sources_sha256") != step_kernel_sources_sha256():
         return None
     return rec["traffic_bytes_per_step"]
 
@@ -392,6 +414,83 @@ def cpu_baseline(opt, params, budget_s=20.0):
                       "elements".format(len(sample), sample_elems, reps, full)}
 
 
+def cpu_baseline_muon(opt, params, budget_s=20.0):
+    """Oracle GefenMuon step (quantised momentum and Nesterov blend in C, the
+    Newton-Schulz products in float64 numpy with a bf16 rounding per torch op,
+    the parameter update) on a sample of matrices, scaled by Newton-Schulz flops
+    to one full step: the CPU restatement of the reference's path
+    (gefen_muon.py:16-51, 132-171, 302-329)."""
+    from oracle import oracle as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+        blas = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except ImportError:
+        blas = 1
+    cb = opt._gefen_codebook.detach().cpu().numpy().astype(np.float32)
+    g0 = opt.param_groups[0]
+    coeffs, steps, eps = tuple(g0["ns_coefficients"]), g0["ns_steps"], g0["eps"]
+
+    def ns_flops(shape):
+        m, n = min(shape), max(shape)
+        return steps * 2.0 * (m * m * n + m * m * m + m * m * n)
+
+    # the first q_proj-like (square) and k_proj-like (1024 x 2048) matrices
+    sample = [next(i for i, (_, p) in enumerate(params) if p.shape[0] == p.shape[1]),
+              next(i for i, (_, p) in enumerate(params) if p.shape[0] < p.shape[1])]
+    host = []
+    for i in sample:
+        _, p = params[i]
+        st = opt.state[p]
+        conv = (lambda t: t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
+        tstate = orc.TensorState(p.numel(), st["automatic_period"], "bf16", "bf16")
+        tstate.m_codebook = st["m_codebook"].cpu().numpy().reshape(-1).copy()
+        tstate.m_magnitude = conv(st["m_magnitude"]).copy()
+        tstate.pod = st.get("period_one_divisor")
+        host.append((i, conv(p).copy(), conv(p.grad).copy(), tstate))
+    reps, elapsed = 0, 0.0
+    while elapsed < budget_s and reps < 5:
+        t0 = time.perf_counter()
+        for i, pp, gg, tstate in host:
+            _, p = params[i]
+            blend = orc.muon_momentum(gg, "bf16", tstate, cb, g0["momentum"], g0["nesterov"])
+            u = orc.newton_schulz_bf16(orc.to_f32(blend, "bf16").reshape(tuple(p.shape)), coeffs, steps, eps)
+            orc.muon_apply(pp, orc.from_f32(u, "bf16"), "bf16", tuple(p.shape), g0["lr"], g0["weight_decay"],
+                           orc.adjust_lr(g0["lr"], g0["adjust_lr_fn"], tuple(p.shape)))
+        elapsed += time.perf_counter() - t0
+        reps += 1
+    per_rep = elapsed / reps
+    scale = sum(ns_flops(tuple(p.shape)) for _, p in params) / sum(ns_flops(tuple(params[i][1].shape))
+                                                                    for i in sample)
+    return {"value": round(per_rep * scale * 1000.0, 1), "unit": "ms per full step (scaled by Newton-Schulz flops)",
+            "cores": blas, "kind": "port",
+            "sample": "{} matrices ({}), {} repetitions of the oracle GefenMuon step (numpy float64 products on {} "
+                      "BLAS threads), scaled by Newton-Schulz flops to all {} matrices".format(
+                          len(sample), ", ".join("{}x{}".format(*params[i][1].shape) for i in sample), reps, blas,
+                          len(params))}
+
+
+def cpu_baseline_kernels(g_host, period_divs):
+    """The same first-step codebook pipeline (period scores of every divisor,
+    histogram, exact DP) on the same 64M-element tensor with the oracle (C,
+    OpenMP for scores and histogram, one thread for the DP)."""
+    from oracle import oracle as orc
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    t0 = time.perf_counter()
+    sc = orc.period_scores(g_host, "f32", period_divs, mode=1)
+    period = orc.finalize_period(list(zip(period_divs, sc.tolist())), g_host.size)
+    t1 = time.perf_counter()
+    counts = orc.histogram(g_host, "f32", period)
+    t2 = time.perf_counter()
+    orc.exact_dp(counts.astype(np.float32), 256, True)
+    t3 = time.perf_counter()
+    return {"value": round((t3 - t0) * 1000.0, 1), "unit": "ms (period scores + histogram + exact DP)",
+            "cores": cores, "kind": "port",
+            "sample": "the whole 64M-element tensor: scores {:.0f} ms, histogram {:.0f} ms, DP {:.0f} ms (one "
+                      "thread)".format((t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -424,6 +523,15 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     params = build_problem(cfg, dev)
+
+    def set_grads(k):
+        """The gradients of step k + 1, written into the same gradient buffers before
+        the step (outside the timed region): every step sees new values at the
+        addresses a training loop's caching allocator typically hands back."""
+        for i, (_, p) in enumerate(params):
+            fill_grad(cfg, p.grad, i, k)
+        torch.cuda.synchronize()
+
     Opt = GefenMuon if cfg["opt"] == "muon" else Gefen
     opt = Opt(params)
     torch.cuda.synchronize()
@@ -431,11 +539,16 @@ def main():
     opt.step()
     torch.cuda.synchronize()
     first_ms = (time.perf_counter() - t0) * 1000.0
+    step_no = 1
     for _ in range(args.warmup):
+        set_grads(step_no)
+        step_no += 1
         opt.step()
     torch.cuda.synchronize()
     times = []
     for _ in range(args.steps):
+        set_grads(step_no)
+        step_no += 1
         t0 = time.perf_counter()
         opt.step()
         torch.cuda.synchronize()
@@ -482,6 +595,8 @@ def main():
             out["cpu_baseline"] = cpu_baseline(opt, params)
     else:
         out["roofline"] = muon_ns_roofline(opt, params)
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_muon(opt, params)
     print(json.dumps(out), flush=True)
 
 
