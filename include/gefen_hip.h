@@ -168,7 +168,8 @@ int gefen_muon_tasks(const gefen_muon_task* tasks, int ntasks, const void* table
  * input of the Frobenius norm that gefen_ns_prepare_sumsq divides by, gathered
  * while the output is written instead of by another pass over it.  sumsq holds
  * GEFEN_SUMSQ_STRIDE float64 entries per task (device, ntasks * GEFEN_SUMSQ_STRIDE
- * entries, set to zero first), of which GEFEN_SUMSQ_SLOTS partial sums, one per
+ * entries, which the call sets to zero on `stream` by a fill kernel before the
+ * momentum launches), of which GEFEN_SUMSQ_SLOTS partial sums, one per
  * 128-byte line: task i's sum is the sum over s of
  * sumsq[i * GEFEN_SUMSQ_STRIDE + 16 * s].  Each workgroup adds its float32 sum
  * to one slot with a float64 atomic, so the last bits may vary between runs;
