@@ -230,15 +230,21 @@ struct TileGemm {
     int d_t;       // D is given as D^T [N, M] (row stride ldd): four rows of one column are one 8-byte load
 };
 
-// The TCH 16-byte chunks of this thread in a 256 x TK operand tile: chunk q =
-// threadIdx.x + TT i is row q / CPR, k-chunk q % CPR.
-__device__ __forceinline__ void tile_load(const uint16_t* __restrict__ src, int64_t ld, int r0, int k0,
-                                          u32x4 out[TCH]) {
+// Buffer resource over the 256 rows of one operand tile (rows r0 .. r0 + 255 of
+// a row-major matrix with row stride ld): the loads address it with a 32-bit
+// per-thread offset and a scalar offset, so no 64-bit address is formed per
+// load (the entry point checks that 256 rows fit in 2^31 bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* rows, int64_t ld) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(rows), (short)0, (int)(TM * ld * 2), 0x00020000);
+}
+// The TCH 16-byte chunks of this thread in a 256 x TK operand tile at column k0:
+// chunk q = threadIdx.x + TT i is row q / CPR, k-chunk q % CPR.  voff is the
+// byte offset of chunk 0 (row threadIdx.x / CPR); chunk i is TT / CPR rows on.
+__device__ __forceinline__ void tile_load(__amdgpu_buffer_rsrc_t rs, int voff, int64_t ld, int k0, u32x4 out[TCH]) {
 #pragma unroll
-    for (int i = 0; i < TCH; ++i) {
-        const int q = threadIdx.x + TT * i;
-        out[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + q / CPR) * ld + k0 + (q % CPR) * 8);
-    }
+    for (int i = 0; i < TCH; ++i)
+        out[i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, (int)(((int64_t)(TT / CPR) * i * ld + k0) * 2), 0));
 }
 __device__ __forceinline__ void tile_store(uint16_t* lds, const u32x4 in[TCH]) {
 #pragma unroll
@@ -319,20 +325,28 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
 
     const int nk = g.K / TK;
     u32x4 ra[TCH], rb[TCH];  // register stage of the global -> LDS pipeline
-    tile_load(A, g.lda, m0, 0, ra);
-    tile_load(B, g.ldb, n0, 0, rb);
+    const __amdgpu_buffer_rsrc_t rsa = tile_rsrc(A + (int64_t)m0 * g.lda, g.lda);
+    const __amdgpu_buffer_rsrc_t rsb = tile_rsrc(B + (int64_t)n0 * g.ldb, g.ldb);
+    const int voa = (int)(((threadIdx.x / CPR) * g.lda + (threadIdx.x % CPR) * 8) * 2);
+    const int vob = (int)(((threadIdx.x / CPR) * g.ldb + (threadIdx.x % CPR) * 8) * 2);
+    tile_load(rsa, voa, g.lda, 0, ra);
+    tile_load(rsb, vob, g.ldb, 0, rb);
     tile_store(As[0], ra);
     tile_store(Bs[0], rb);
     if (nk > 1) {
-        tile_load(A, g.lda, m0, TK, ra);
-        tile_load(B, g.ldb, n0, TK, rb);
+        tile_load(rsa, voa, g.lda, TK, ra);
+        tile_load(rsb, vob, g.ldb, TK, rb);
     }
     __syncthreads();
     // One K step from LDS stage CUR.  It first stores step kt + 1 (loaded during
     // step kt - 1) into the other LDS stage, which every wave finished reading
     // before the last barrier, then reloads the registers with step kt + 2
     // (clamped to the last step: the loads are unconditional).  Fragments of the
-    // next 16-deep slice are read while the current slice's MFMAs run.  (A
+    // next 16-deep slice are read while the current slice's MFMAs run, in the
+    // order GEFEN_SCHED_STEP fixes: the first slice's fragments, then each MFMA
+    // followed by one fragment read of the next slice and, during the first
+    // slice, one of the step's global loads.  (Left to the compiler, the loads
+    // sank to the end of the step and the reads bunched up: 8% slower.  A
     // second register stage, loads two steps ahead with the stores after the
     // MFMAs, measured 5% slower: the stores then wait at the end of every step.)
 #define GEFEN_LOAD_FRAGS(AS, BS, KK, AF, BF)                                                                      \
@@ -345,6 +359,18 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
 #define GEFEN_MFMAS(AF, BF)                                                                                       \
     _Pragma("unroll") for (int i = 0; i < WI; ++i) _Pragma("unroll") for (int j = 0; j < WJ; ++j) acc[i][j] =     \
         __builtin_amdgcn_mfma_f32_32x32x16_bf16(AF[i], BF[j], acc[i][j], 0, 0, 0);
+    // instruction groups in issue order (masks: 0x008 MFMA, 0x100 LDS read, 0x020 global read)
+#define GEFEN_SCHED_STEP                                                                                          \
+    {                                                                                                             \
+        __builtin_amdgcn_sched_group_barrier(0x100, WI + WJ, 0);                                                  \
+        _Pragma("unroll") for (int s_ = 0; s_ < TK / 16; ++s_) {                                                  \
+            _Pragma("unroll") for (int t_ = 0; t_ < WI * WJ; ++t_) {                                              \
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                \
+                if (s_ + 1 < TK / 16 && t_ < WI + WJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          \
+                if (s_ == 0 && t_ < 2 * TCH) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                   \
+            }                                                                                                     \
+        }                                                                                                         \
+    }
 #define GEFEN_TILE_STEP(KT, CUR)                                                                                  \
     {                                                                                                             \
         if ((KT) + 1 < nk) {                                                                                      \
@@ -352,8 +378,8 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
             tile_store(Bs[(CUR) ^ 1], rb);                                                                        \
         }                                                                                                         \
         const int kpre = min((KT) + 2, nk - 1) * TK;                                                              \
-        tile_load(A, g.lda, m0, kpre, ra);                                                                        \
-        tile_load(B, g.ldb, n0, kpre, rb);                                                                        \
+        tile_load(rsa, voa, g.lda, kpre, ra);                                                                     \
+        tile_load(rsb, vob, g.ldb, kpre, rb);                                                                     \
         const uint16_t* as = As[CUR];                                                                             \
         const uint16_t* bs = Bs[CUR];                                                                             \
         bf16x8 af0[WI], bf0[WJ], af1[WI], bf1[WJ];                                                                \
@@ -364,6 +390,7 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
             if (kk + 32 < TK) GEFEN_LOAD_FRAGS(as, bs, kk + 32, af0, bf0)                                         \
             GEFEN_MFMAS(af1, bf1)                                                                                 \
         }                                                                                                         \
+        GEFEN_SCHED_STEP                                                                                          \
         lds_barrier();                                                                                            \
     }
     int kt = 0;
@@ -373,6 +400,7 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     }
     if (kt < nk) GEFEN_TILE_STEP(kt, 0)
 #undef GEFEN_TILE_STEP
+#undef GEFEN_SCHED_STEP
 #undef GEFEN_MFMAS
 #undef GEFEN_LOAD_FRAGS
     // epilogue: C = alpha * acc + beta * D rounded once, assembled in LDS as
@@ -517,6 +545,8 @@ extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t st
         return fail_inval("GEMM leading dimension too small");
     if (symmetric && m != n) return fail_inval("a symmetric GEMM must be square");
     if (symmetric && ct) return fail_inval("a symmetric GEMM has no separate transposed output (C^T = C)");
+    if ((int64_t)ns::TM * lda * 2 > INT32_MAX || (int64_t)ns::TN * ldb * 2 > INT32_MAX)
+        return fail_inval("batched GEMM operand rows too long (256 rows must span less than 2^31 bytes)");
     if (m % ns::TM || n % ns::TN || k % ns::TK || k == 0)
         return fail_inval("batched GEMM needs M, N multiples of 256 and K a multiple of %d (got %d, %d, %d)", ns::TK, m, n, k);
     const void* ptrs[5] = {a, b, c, ct, d};
