@@ -50,6 +50,16 @@ def test_entry_points_reject_invalid_arguments_without_a_device():
                                                                0.5, 0.5, 1e-8, None))
     with pytest.raises(ValueError, match="beta2"):
         _lib.check(lib.gefen_automatic_vmean_update(1, 0, 1, 0, 4, 4, 1.5, None))
+    # the batched Newton-Schulz GEMM addresses a 256-row operand tile with 32-bit
+    # byte offsets: rows of 2^22 bf16 elements are refused before any launch
+    # (the pointers are never dereferenced: the checks precede every device call)
+    long_ld = 1 << 22
+    with pytest.raises(ValueError, match="rows too long"):
+        _lib.check(lib.gefen_gemm_bf16_nt_batched(256, long_ld, 0, 256, 256, 0, 256, 256, 0, None, 0, 0, None, 0, 0,
+                                                  0, 1, 256, 256, 256, 1.0, 0.0, 0, None))
+    with pytest.raises(ValueError, match="multiples of 256"):
+        _lib.check(lib.gefen_gemm_bf16_nt_batched(256, 320, 0, 256, 320, 0, 256, 320, 0, None, 0, 0, None, 0, 0,
+                                                  0, 1, 320, 320, 320, 1.0, 0.0, 0, None))
     assert lib.gefen_exact_dp_workspace_size(4096, 256) > 256 * 4097 * 12
 
 
