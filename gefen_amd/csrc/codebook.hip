@@ -155,29 +155,65 @@ struct DpLayout {
     }
 };
 
-__global__ void k_dp_init(const float* __restrict__ counts, int bins, int K, int force, char* __restrict__ ws,
-                          DpLayout L, float* __restrict__ out) {
+constexpr int kDpMaxBins = 4096;
+constexpr int kDpInitThreads = 256;
+
+// Active bins (count > 0) in bin order, their centres -1 + (2b+1)/bins (exact
+// for power-of-two bins), and the float64 prefix sums of w, w x, w x^2
+// (torch.cumsum on the CPU, quantization.py:226-231: the element products in
+// parallel, then the sums in sequential order).  The workgroup compacts the
+// active bins into LDS (a scan of per-thread counts); one thread then runs the
+// three running sums in registers.
+__global__ __launch_bounds__(kDpInitThreads) void k_dp_init(const float* __restrict__ counts, int bins, int K,
+                                                            int force, char* __restrict__ ws, DpLayout L,
+                                                            float* __restrict__ out) {
+    constexpr int kPer = kDpMaxBins / kDpInitThreads;  // bins per thread
+    __shared__ double sw_[kDpMaxBins], swx_[kDpMaxBins], swx2_[kDpMaxBins];
+    __shared__ int offs[kDpInitThreads + 1];
     int32_t* hdr = reinterpret_cast<int32_t*>(ws);
     double* pw = reinterpret_cast<double*>(ws + L.pw);
     double* pwx = reinterpret_cast<double*>(ws + L.pwx);
     double* pwx2 = reinterpret_cast<double*>(ws + L.pwx2);
     double* dp = reinterpret_cast<double*>(ws + L.dp);
     float* cw = reinterpret_cast<float*>(ws + L.cw);
-    if (threadIdx.x != 0) return;
-    // active bins in bin order; centres -1 + (2b+1)/bins are exact for power-of-two bins
-    int N = 0;
-    pw[0] = 0.0; pwx[0] = 0.0; pwx2[0] = 0.0;
-    for (int b = 0; b < bins; ++b) {
+    const int t = threadIdx.x;
+    const int b0 = t * kPer;  // this thread's bins b0 .. b0 + kPer - 1 (in order)
+    int mine = 0;
+    for (int k = 0; k < kPer; ++k) mine += (b0 + k < bins && counts[b0 + k] > 0.0f) ? 1 : 0;
+    offs[t + 1] = mine;
+    if (t == 0) offs[0] = 0;
+    __syncthreads();
+    if (t == 0)
+        for (int i = 1; i <= kDpInitThreads; ++i) offs[i] += offs[i - 1];
+    __syncthreads();
+    const double inv_bins = 1.0 / (double)bins;  // exact: bins is a power of two
+    int n = offs[t];
+    for (int k = 0; k < kPer; ++k) {
+        const int b = b0 + k;
+        if (b >= bins) break;
         const float c = counts[b];
         if (c > 0.0f) {
-            const float center = (float)(-1.0 + (2.0 * b + 1.0) / (double)bins);
+            const float center = (float)(-1.0 + (2.0 * b + 1.0) * inv_bins);
             const double w = (double)c, x = (double)center;
-            pw[N + 1] = pw[N] + w;
-            pwx[N + 1] = pwx[N] + w * x;
-            pwx2[N + 1] = pwx2[N] + w * (x * x);
-            cw[N] = center;
-            ++N;
+            sw_[n] = w;
+            swx_[n] = w * x;
+            swx2_[n] = w * (x * x);
+            cw[n] = center;
+            ++n;
         }
+    }
+    __syncthreads();
+    if (t != 0) return;
+    const int N = offs[kDpInitThreads];
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0;
+    pw[0] = 0.0; pwx[0] = 0.0; pwx2[0] = 0.0;
+    for (int i = 0; i < N; ++i) {
+        a0 = a0 + sw_[i];
+        a1 = a1 + swx_[i];
+        a2 = a2 + swx2_[i];
+        pw[i + 1] = a0;
+        pwx[i + 1] = a1;
+        pwx2[i + 1] = a2;
     }
     hdr[0] = N;
     if (N == 0) { hdr[1] = 2; return; }
@@ -197,63 +233,121 @@ __global__ void k_dp_init(const float* __restrict__ counts, int bins, int K, int
     dp[0] = 0.0;
     for (int e = 1; e <= N; ++e) dp[e] = __builtin_inf();
 }
+static_assert(kDpMaxBins % kDpInitThreads == 0, "whole bins per thread");
 
-// one level c: dp[c][e] = min_s dp[c-1][s-1] + cost(s, e), one wave per e
-__global__ __launch_bounds__(256) void k_dp_level(int c, int K, int force, int bins, char* __restrict__ ws,
-                                                  DpLayout L) {
-    const int32_t* hdr = reinterpret_cast<const int32_t*>(ws);
-    if (hdr[1] != 0) return;
-    const int N = hdr[0];
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const size_t stride = (size_t)bins + 1;
-    const double* pw = reinterpret_cast<const double*>(ws + L.pw);
-    const double* pwx = reinterpret_cast<const double*>(ws + L.pwx);
-    const double* pwx2 = reinterpret_cast<const double*>(ws + L.pwx2);
-    double* dp = reinterpret_cast<double*>(ws + L.dp);
-    int32_t* bt = reinterpret_cast<int32_t*>(ws + L.bt);
-    if (e > N) return;  // whole wave
-    const double* prev = dp + (size_t)(c - 1) * stride;
-    if (e < c) {
-        if (lane == 0) { dp[(size_t)c * stride + e] = __builtin_inf(); bt[(size_t)c * stride + e] = -1; }
-        return;
+// One DP level (quantization.py:158-186): for every segment end e in [c, N],
+// the first start s in [c, e] minimising dp[c-1][s-1] + cost(s, e), in
+// float64 with the reference's expression order; strict < keeps the first
+// minimum, and the cross-lane reduction takes the lexicographic (cost, start)
+// minimum.  The prefix sums and the previous level are staged in LDS (4 x
+// (N + 1) doubles, 131 KB at N = 4096) and every candidate reads them from
+// there.  Wave p of the grid takes the ends c + p and N - p, whose candidate
+// counts add up to N - c + 2, so the waves carry equal work.
+constexpr int kDpThreads = 512;
+constexpr int kDpWaves = kDpThreads / 64;
+static_assert(4 * (kDpMaxBins + 1) * sizeof(double) <= 160 * 1024, "the staged arrays fit in the LDS of one CU");
+
+// Segment cost of starts s (prefix index s - 1) for end e: MODE 0 the
+// free-centre cost sum_wx2 - sum_wx^2 / sum_w, MODE -1 / +1 the cost about
+// the fixed centre -1 / +1 (force_endpoints, first / last cluster).
+template <int MODE>
+__device__ __forceinline__ double dp_cost(double Pe, double PXe, double PX2e, const double* spw, const double* spwx,
+                                          const double* spwx2, int i) {
+    const double sw = Pe - spw[i];
+    const double swx = PXe - spwx[i];
+    const double swx2 = PX2e - spwx2[i];
+    if (MODE == 0) {
+        const double sq = swx * swx;
+        return swx2 - sq / sw;
     }
-    const bool fixed_lo = force && c == 1;
-    const bool fixed_hi = force && c == K;
-    const double Pe = pw[e], PXe = pwx[e], PX2e = pwx2[e];
-    double best = __builtin_inf();
-    int bs = -1;
-    for (int s = c + lane; s <= e; s += 64) {
-        const double sw = Pe - pw[s - 1];
-        const double swx = PXe - pwx[s - 1];
-        const double swx2 = PX2e - pwx2[s - 1];
-        double cost;
-        if (fixed_lo) {
-            const double fc = -1.0;
-            const double t1 = (2.0 * fc) * swx;
-            const double t2 = (fc * fc) * sw;
-            cost = (swx2 - t1) + t2;
-        } else if (fixed_hi) {
-            const double fc = 1.0;
-            const double t1 = (2.0 * fc) * swx;
-            const double t2 = (fc * fc) * sw;
-            cost = (swx2 - t1) + t2;
-        } else {
-            const double sq = swx * swx;
-            cost = swx2 - sq / sw;
+    const double fc = (double)MODE;
+    const double t1 = (2.0 * fc) * swx;
+    const double t2 = (fc * fc) * sw;
+    return (swx2 - t1) + t2;
+}
+
+// Best start for end e over this lane's starts s = c + lane + 64 j, in
+// ascending order (strict < keeps the first minimum); kDpUnroll independent
+// candidates per iteration.
+#ifndef GEFEN_DP_UNROLL
+#define GEFEN_DP_UNROLL 4
+#endif
+constexpr int kDpUnroll = GEFEN_DP_UNROLL;
+template <int MODE>
+__device__ __forceinline__ void dp_scan(int e, int c, int lane, const double* spw, const double* spwx,
+                                        const double* spwx2, const double* sprev, double& best, int& bs) {
+    const double Pe = spw[e], PXe = spwx[e], PX2e = spwx2[e];
+    int s = c + lane;
+    for (; s + 64 * (kDpUnroll - 1) <= e; s += 64 * kDpUnroll) {
+        double cand[kDpUnroll];
+#pragma unroll
+        for (int u = 0; u < kDpUnroll; ++u) {
+            const int i = s + 64 * u - 1;
+            cand[u] = sprev[i] + dp_cost<MODE>(Pe, PXe, PX2e, spw, spwx, spwx2, i);
         }
-        const double cand = prev[s - 1] + cost;
+#pragma unroll
+        for (int u = 0; u < kDpUnroll; ++u)
+            if (cand[u] < best) { best = cand[u]; bs = s + 64 * u; }
+    }
+    for (; s <= e; s += 64) {
+        const double cand = sprev[s - 1] + dp_cost<MODE>(Pe, PXe, PX2e, spw, spwx, spwx2, s - 1);
         if (cand < best) { best = cand; bs = s; }
     }
-    // lexicographic (cost, start) minimum over the wave; -1 means no candidate
+}
+
+__device__ __forceinline__ void dp_end(int e, int c, int K, int force, int lane, const double* spw, const double* spwx,
+                                       const double* spwx2, const double* sprev, double* dpc, int32_t* btc) {
+    double best = __builtin_inf();
+    int bs = -1;
+    if (force && c == 1) dp_scan<-1>(e, c, lane, spw, spwx, spwx2, sprev, best, bs);
+    else if (force && c == K) dp_scan<1>(e, c, lane, spw, spwx, spwx2, sprev, best, bs);
+    else dp_scan<0>(e, c, lane, spw, spwx, spwx2, sprev, best, bs);
     for (int off = 32; off > 0; off >>= 1) {
         const double ob = __shfl_xor(best, off, 64);
         const int os = __shfl_xor(bs, off, 64);
         if (os >= 0 && (bs < 0 || ob < best || (ob == best && os < bs))) { best = ob; bs = os; }
     }
     if (lane == 0) {
-        dp[(size_t)c * stride + e] = bs >= 0 ? best : __builtin_inf();
-        bt[(size_t)c * stride + e] = bs;
+        dpc[e] = bs >= 0 ? best : __builtin_inf();
+        btc[e] = bs;
+    }
+}
+
+__global__ __launch_bounds__(kDpThreads) void k_dp_level(int c, int K, int force, int bins, char* __restrict__ ws,
+                                                         DpLayout L) {
+    __shared__ double spw[kDpMaxBins + 1], spwx[kDpMaxBins + 1], spwx2[kDpMaxBins + 1], sprev[kDpMaxBins + 1];
+    const int32_t* hdr = reinterpret_cast<const int32_t*>(ws);
+    if (hdr[1] != 0) return;
+    const int N = hdr[0];
+    const size_t stride = (size_t)bins + 1;
+    const double* pw = reinterpret_cast<const double*>(ws + L.pw);
+    const double* pwx = reinterpret_cast<const double*>(ws + L.pwx);
+    const double* pwx2 = reinterpret_cast<const double*>(ws + L.pwx2);
+    double* dp = reinterpret_cast<double*>(ws + L.dp);
+    int32_t* bt = reinterpret_cast<int32_t*>(ws + L.bt);
+    const double* prev = dp + (size_t)(c - 1) * stride;
+    double* dpc = dp + (size_t)c * stride;
+    int32_t* btc = bt + (size_t)c * stride;
+    if (blockIdx.x == 0) {  // ends below c have no segmentation into c clusters
+        for (int e = threadIdx.x; e < c && e <= N; e += kDpThreads) {
+            dpc[e] = __builtin_inf();
+            btc[e] = -1;
+        }
+    }
+    const int cnt = N - c + 1;  // ends c .. N
+    if (blockIdx.x > 0 && 2 * (int)blockIdx.x * kDpWaves >= cnt) return;  // no pair of ends here (uniform)
+    // indices c - 1 .. N of the four arrays (s - 1 >= c - 1, e <= N)
+    for (int i = c - 1 + (int)threadIdx.x; i <= N; i += kDpThreads) {
+        spw[i] = pw[i];
+        spwx[i] = pwx[i];
+        spwx2[i] = pwx2[i];
+        sprev[i] = prev[i];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    for (int p = blockIdx.x * kDpWaves + (int)(threadIdx.x >> 6); 2 * p < cnt; p += gridDim.x * kDpWaves) {
+        dp_end(c + p, c, K, force, lane, spw, spwx, spwx2, sprev, dpc, btc);
+        if (N - p != c + p) dp_end(N - p, c, K, force, lane, spw, spwx, spwx2, sprev, dpc, btc);
     }
 }
 
@@ -486,13 +580,14 @@ extern "C" int gefen_exact_dp(const float* counts, int bins, int codebook_size, 
     DpLayout L(bins, K);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
-    hipLaunchKernelGGL(k_dp_init, dim3(1), dim3(64), 0, st, counts, bins, K, force_endpoints ? 1 : 0, ws, L,
-                       codebook_out);
+    hipLaunchKernelGGL(k_dp_init, dim3(1), dim3(kDpInitThreads), 0, st, counts, bins, K, force_endpoints ? 1 : 0,
+                       ws, L, codebook_out);
     int rc = launch_status("gefen_exact_dp init");
     if (rc) return rc;
-    const int grid = (bins + 1 + 3) / 4;
+    // enough waves for one pair of ends each at the largest level width (bins ends)
+    const int grid = bins / 2 >= kDpWaves ? (bins / 2 + kDpWaves - 1) / kDpWaves : 1;
     for (int c = 1; c <= K; ++c) {
-        hipLaunchKernelGGL(k_dp_level, dim3(grid), dim3(256), 0, st, c, K, force_endpoints ? 1 : 0, bins, ws, L);
+        hipLaunchKernelGGL(k_dp_level, dim3(grid), dim3(kDpThreads), 0, st, c, K, force_endpoints ? 1 : 0, bins, ws, L);
         rc = launch_status("gefen_exact_dp level");
         if (rc) return rc;
     }

@@ -79,6 +79,33 @@ def test_exact_dp_full_histogram_matches_oracle():
     np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("case", ["sparse_k256", "sparse_k16_free", "edges_k64", "few_bins_padded"])
+def test_exact_dp_sparse_histograms_match_oracle(case):
+    """Histograms whose active bins are scattered over the 4096 bins (runs of
+    empty bins across the init kernel's per-thread bin ranges of 16, active
+    first and last bins, fewer active bins than codebook entries), against the
+    C oracle: the compaction keeps bin order and the prefix sums stay sequential."""
+    from gefen_amd.quantization import exact_dp_from_counts
+
+    rng = np.random.default_rng(17)
+    counts = np.zeros(4096, np.float32)
+    if case in ("sparse_k256", "sparse_k16_free"):
+        active = rng.random(4096) < 0.3
+        active[rng.integers(0, 4096 - 200):][:200] = False  # a long empty run
+        counts[active] = rng.integers(1, 5000, int(active.sum())).astype(np.float32)
+        k, force = (256, True) if case == "sparse_k256" else (16, False)
+    elif case == "edges_k64":
+        counts[[0, 15, 16, 17, 1000, 2047, 2048, 4080, 4095]] = [3, 1, 7, 2, 9, 4, 4, 5, 6]
+        counts[np.arange(100, 4000, 37)] = rng.integers(1, 50, len(range(100, 4000, 37)))
+        k, force = 64, True
+    else:
+        counts[[5, 300, 301, 3000]] = [2, 8, 1, 4]
+        k, force = 16, True
+    ref = orc.exact_dp(counts, k, force)
+    got = exact_dp_from_counts(torch.from_numpy(counts).to("cuda:0"), k, force).cpu().numpy()
+    np.testing.assert_array_equal(got, ref, err_msg=case)
+
+
 def test_learned_codebook_pipeline_matches_reference():
     from gefen_amd.gefen import learn_gefen_exact_codebook_from_grad_periods
 
