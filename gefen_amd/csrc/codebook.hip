@@ -203,18 +203,45 @@ __global__ __launch_bounds__(kDpInitThreads) void k_dp_init(const float* __restr
         }
     }
     __syncthreads();
-    if (t != 0) return;
     const int N = offs[kDpInitThreads];
-    double a0 = 0.0, a1 = 0.0, a2 = 0.0;
-    pw[0] = 0.0; pwx[0] = 0.0; pwx2[0] = 0.0;
-    for (int i = 0; i < N; ++i) {
-        a0 = a0 + sw_[i];
-        a1 = a1 + swx_[i];
-        a2 = a2 + swx2_[i];
-        pw[i + 1] = a0;
-        pwx[i + 1] = a1;
-        pwx2[i + 1] = a2;
+    if (t == 0) {  // the running sums in bin order, in place in LDS (16 elements read ahead)
+        constexpr int kB = 16;
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0;
+        int i = 0;
+        for (; i + kB <= N; i += kB) {
+            double v0[kB], v1[kB], v2[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) { v0[u] = sw_[i + u]; v1[u] = swx_[i + u]; v2[u] = swx2_[i + u]; }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                a0 = a0 + v0[u];
+                a1 = a1 + v1[u];
+                a2 = a2 + v2[u];
+                v0[u] = a0;
+                v1[u] = a1;
+                v2[u] = a2;
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) { sw_[i + u] = v0[u]; swx_[i + u] = v1[u]; swx2_[i + u] = v2[u]; }
+        }
+        for (; i < N; ++i) {
+            a0 = a0 + sw_[i];
+            a1 = a1 + swx_[i];
+            a2 = a2 + swx2_[i];
+            sw_[i] = a0;
+            swx_[i] = a1;
+            swx2_[i] = a2;
+        }
     }
+    __syncthreads();
+    for (int i = t; i <= N; i += kDpInitThreads) {
+        pw[i] = i ? sw_[i - 1] : 0.0;
+        pwx[i] = i ? swx_[i - 1] : 0.0;
+        pwx2[i] = i ? swx2_[i - 1] : 0.0;
+    }
+    if (N > 0 && K <= N)  // dp[0][e]: no segmentation of e > 0 points into zero clusters
+        for (int e = t; e <= N; e += kDpInitThreads) dp[e] = e ? __builtin_inf() : 0.0;
+    if (t != 0) return;
     hdr[0] = N;
     if (N == 0) { hdr[1] = 2; return; }
     if (K > N) {  // quantization.py:68-81 padded codebook
@@ -230,8 +257,6 @@ __global__ __launch_bounds__(kDpInitThreads) void k_dp_init(const float* __restr
         return;
     }
     hdr[1] = 0;
-    dp[0] = 0.0;
-    for (int e = 1; e <= N; ++e) dp[e] = __builtin_inf();
 }
 static_assert(kDpMaxBins % kDpInitThreads == 0, "whole bins per thread");
 
