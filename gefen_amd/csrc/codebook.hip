@@ -87,6 +87,21 @@ __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restric
     atomicMax(&probe_max, worst);
     __syncthreads();
     if (t == 0) T->max_probe = (bk[0] != 0) ? 1 << 20 : probe_max;
+    // nb16: #{k in 1..K-1 : thr[k] < x} for the bf16 values x of the table
+    for (int i = t; i < kNb16Bytes; i += 256) {
+        uint8_t c = 0;
+        if (i < 2 * (int)kNb16Side) {
+            const uint32_t bits = (i < (int)kNb16Side ? 0u : 0x8000u) | (kNb16Lo + (uint32_t)i % kNb16Side);
+            const float x = __uint_as_float(bits << 16);
+            int lo = 1, hi = K;  // first k in [1, K) with thr[k] >= x
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (thr[mid] < x) lo = mid + 1; else hi = mid;
+            }
+            c = (uint8_t)(lo - 1);
+        }
+        T->nb16[i] = c;
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -150,6 +150,12 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 //            use the fixed two-probe search.
 //   bucket8  the same counts as bytes (every count is <= 255), padded with zeros
 //            to 4112 entries: the compact copy the step kernels keep in LDS.
+//   nb16[i]  the nearest index of the bf16 value with bits kNb16Lo + i (i < kNb16Side)
+//            and of its negative (entry kNb16Side + i): every bf16 x with
+//            2^-20 <= |x| <= 1.0078125, the range of the GefenMuon quotients.
+constexpr uint32_t kNb16Lo = 0x3580u;                 // 2^-20
+constexpr uint32_t kNb16Side = 0x3F82u - kNb16Lo;     // up to 0x3F81 = 1.0078125
+constexpr int kNb16Bytes = (2 * kNb16Side + 15) / 16 * 16;
 struct CodebookTables {
     float cb[256];
     float thr[260];
@@ -158,6 +164,7 @@ struct CodebookTables {
     int32_t K;
     int32_t max_probe;
     int32_t pad[2];
+    alignas(16) uint8_t nb16[kNb16Bytes];
 };
 
 // Nearest codebook index (gefen.py:122-143) from LDS copies of thr and bucket.

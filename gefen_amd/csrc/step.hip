@@ -115,7 +115,8 @@ struct alignas(16) LdsTables {
     uint8_t bucket[4112];
     float cbd[256];
 };
-static_assert(offsetof(CodebookTables, thr) % 16 == 0 && offsetof(CodebookTables, bucket8) % 16 == 0,
+static_assert(offsetof(CodebookTables, thr) % 16 == 0 && offsetof(CodebookTables, bucket8) % 16 == 0 &&
+                  offsetof(CodebookTables, nb16) % 16 == 0,
               "codebook tables must allow 16-byte copies");
 
 // The LDS tables are 386 16-byte pieces: thr and bucket8 follow each other in
@@ -132,17 +133,21 @@ static_assert(offsetof(CodebookTables, thr) == 1024 && offsetof(CodebookTables, 
 // loaded with the codebook tables (root != nullptr).
 constexpr int kRootTab = 384;
 
-template <typename D, int NT>
+// NB16: also copy the bf16 nearest-index table (CodebookTables::nb16) to nb16_lds.
+template <typename D, int NT, bool NB16 = false>
 __device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* T, int& K,
-                                            const float* root = nullptr, float* root_lds = nullptr) {
+                                            const float* root = nullptr, float* root_lds = nullptr,
+                                            uint8_t* nb16_lds = nullptr) {
     using U4 = RawVec<16>::type;
     constexpr int kPieces = 386, kPer = (kPieces + NT - 1) / NT;
     constexpr int kRootPieces = kRootTab * 4 / 16;
+    constexpr int kNbPieces = kNb16Bytes / 16, kNbPer = NB16 ? (kNbPieces + NT - 1) / NT : 0;
     static_assert(NT >= kRootPieces, "one root-table piece per thread");
     K = T->K;
     const U4* src = reinterpret_cast<const U4*>(T);
     U4* dst = reinterpret_cast<U4*>(&L);
     U4 v[kPer];
+    U4 nv[kNbPer > 0 ? kNbPer : 1];
     U4 rv;
     const bool has_root = root != nullptr && threadIdx.x < kRootPieces;
     if (has_root) rv = reinterpret_cast<const U4*>(root)[threadIdx.x];
@@ -151,7 +156,17 @@ __device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* 
         const int q = threadIdx.x + r * NT;
         if (q < kPieces) v[r] = src[q < 322 ? q + 64 : q - 322];
     }
+#pragma unroll
+    for (int r = 0; r < kNbPer; ++r) {
+        const int q = threadIdx.x + r * NT;
+        if (q < kNbPieces) nv[r] = reinterpret_cast<const U4*>(T->nb16)[q];
+    }
     if (has_root) reinterpret_cast<U4*>(root_lds)[threadIdx.x] = rv;
+#pragma unroll
+    for (int r = 0; r < kNbPer; ++r) {
+        const int q = threadIdx.x + r * NT;
+        if (q < kNbPieces) reinterpret_cast<U4*>(nb16_lds)[q] = nv[r];
+    }
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
         const int q = threadIdx.x + r * NT;
@@ -627,10 +642,12 @@ __device__ __forceinline__ float muon_out(float q, float gf, const MuonTask& T) 
 // gradient term, so the element loops look them up instead of recomputing.
 template <typename D, typename S, int W, int R, bool TAB>
 __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
+    constexpr bool kNb = std::is_same<D, bf16_t>::value;  // bf16 quotients: the nb16 table
     __shared__ LdsTables L;
     __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
+    __shared__ __attribute__((aligned(16))) uint8_t nb16[kNb ? kNb16Bytes : 16];
     int K;
-    load_tables<D, kThreads>(L, B.tables, K);
+    load_tables<D, kThreads, kNb>(L, B.tables, K, nullptr, nullptr, nb16);
     const int ti = find_task(B.wg_begin, B.ntasks);
     const MuonTask& T = B.t[ti];
     const bool two_probe = B.tables->max_probe <= 2;
@@ -718,21 +735,47 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         float sq = 0.0f;  // sum of squares of the outputs this lane writes
+        // every row of the wave fast (wave-uniform): the branch-free search below
+        const bool all_fast = __builtin_amdgcn_ballot_w64(!fast) == 0;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             Vec<uint8_t, W> io;
             Vec<D, W> oo;
             float sqj = 0.0f;
+            int kw[W];
+            if (kNb && all_fast) {
+                // the bf16 quotient's bits index nb16 directly; a quotient outside
+                // the table (|x| < 2^-20) takes the two-probe search, once per wave
+                uint32_t miss = 0;
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const uint32_t xb = from_f32<bf16_t>(div_by_block(mu[j][w], rb)).bits;
+                    const uint32_t off = (xb & 0x7fffu) - kNb16Lo;
+                    const bool hit = off < kNb16Side;
+                    kw[w] = nb16[hit ? off + ((xb & 0x8000u) ? kNb16Side : 0u) : 0u];
+                    miss |= hit ? 0u : (1u << w);
+                }
+                if (__builtin_amdgcn_ballot_w64(miss != 0) != 0) {
+#pragma unroll
+                    for (int w = 0; w < W; ++w)
+                        if (miss & (1u << w))
+                            kw[w] = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    if (fast) {
+                        kw[w] = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
+                    } else {
+                        float x = round_to<D>(mu[j][w] / clamped);  // div_
+                        if (ms <= 0.0f) x = 0.0f;                   // masked_fill_(mag <= 0)
+                        kw[w] = nearest_fast(x, L.thr, L.bucket, K);
+                    }
+                }
+            }
 #pragma unroll
             for (int w = 0; w < W; ++w) {
-                int k;
-                if (fast) {
-                    k = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
-                } else {
-                    float x = round_to<D>(mu[j][w] / clamped);  // div_
-                    if (ms <= 0.0f) x = 0.0f;                   // masked_fill_(mag <= 0)
-                    k = nearest_fast(x, L.thr, L.bucket, K);
-                }
+                const int k = kw[w];
                 io.v[w] = (uint8_t)k;
                 const float a = TAB ? otab[k] : out_base(k);
                 oo.v[w] = from_f32<D>(muon_blend<D>(a, to_f32(gv[j].v[w]), T));

@@ -385,3 +385,50 @@ def test_muon_momentum_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, 
         got = gu.to_np(out_dev)
         both_nan = np.isnan(orc.to_f32(got, dt)) & np.isnan(orc.to_f32(ref, dt))
         np.testing.assert_array_equal(np.where(both_nan, 0, got), np.where(both_nan, 0, ref), err_msg="out step {}".format(step))
+
+
+@pytest.mark.parametrize("cbkind", ["learned", "zero_threshold"])
+@pytest.mark.parametrize("block", [2048, 256])
+def test_muon_momentum_quotients_across_forty_octaves(cbkind, block):
+    """bf16 GefenMuon momentum whose quotients x = m / magnitude spread over
+    2^-40 .. 1 (gradients sign * 2^e, e uniform in [-40, 0]): the bf16 nearest
+    table covers 2^-20 <= |x| <= 1.0078 and the rest takes the two-probe search.
+    With a codebook whose decision threshold between its two middle entries is
+    0 (linspace(-1, 1, 256)), +-tiny quotients and zeros land on either side.
+    Bit-exact against the oracle over three steps."""
+    print("muon octaves", cbkind, block, flush=True)
+    if cbkind == "learned":
+        data, _ = load("exact_dp")
+        cb = np.ascontiguousarray(data["hist_k256_forced/codebook"], dtype=np.float32)
+    else:
+        cb = np.linspace(-1.0, 1.0, 256).astype(np.float32)
+    rows = 16
+    n = rows * block
+    rng = np.random.default_rng(block)
+    idx_np = np.zeros(n, np.uint8)
+    mag_np = np.zeros(rows, np.uint16)
+    idx_dev = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+    mag_dev = torch.zeros(rows, dtype=torch.bfloat16, device="cuda:0")
+    tables = _tables(torch.from_numpy(cb).to("cuda:0"))
+    lib = _lib.load()
+    for step in range(1, 4):
+        e = rng.integers(-40, 1, n).astype(np.float64)
+        g32 = (np.where(rng.random(n) < 0.5, -1.0, 1.0) * np.exp2(e) * (1.0 + rng.random(n))).astype(np.float32)
+        g32[rng.random(n) < 0.01] = 0.0
+        g = syn.round_to(g32, "bf16").reshape(-1).copy()
+        g_dev = gu.to_dev(g, "bf16")
+        out_dev = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
+        task = np.zeros(1, dtype=_lib.MUON_TASK)
+        task["grad"], task["m_codebook"], task["m_magnitude"] = g_dev.data_ptr(), idx_dev.data_ptr(), mag_dev.data_ptr()
+        task["out"], task["numel"], task["block"] = out_dev.data_ptr(), n, block
+        task["grad_dtype"] = task["state_dtype"] = gu.CODE["bf16"]
+        task["momentum"], task["nesterov"] = 0.95, 1
+        _lib.check(lib.gefen_muon_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
+        ref = np.empty(n, dtype=np.uint16)
+        assert orc.lib().orc_muon_momentum(gu.CODE["bf16"], gu.CODE["bf16"], orc._ptr(g), orc._ptr(idx_np),
+                                           orc._ptr(mag_np), orc._ptr(ref), n, block, orc._ptr(cb), cb.size,
+                                           0.95, 1) == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(gu.to_np(idx_dev), idx_np, err_msg="idx step {}".format(step))
+        np.testing.assert_array_equal(gu.to_np(mag_dev), mag_np, err_msg="mag step {}".format(step))
+        np.testing.assert_array_equal(gu.to_np(out_dev), ref, err_msg="out step {}".format(step))
