@@ -96,13 +96,16 @@ __device__ __forceinline__ float divisor_from_sumsq(double s, float eps_bf16) {
 // quotient is the float64 product with 1 / d_g rounded to float (the IEEE
 // quotient: see div_by_block), then rounded to bf16 as torch's bf16 div_ does.
 constexpr int kTile = 64;
+// TPW tiles of one row band per workgroup (the divisor is formed once): two
+// when cols is a multiple of 128 (8% faster on the GefenMuon stacks), else one.
+template <int TPW>
 __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ x, uint16_t* __restrict__ xt,
                                                          int rows, int cols, const float* __restrict__ div,
                                                          const double* __restrict__ sumsq,
                                                          const int32_t* __restrict__ index, float eps_bf16) {
     __shared__ uint16_t tile[kTile][kTile + 2];
     const int g = blockIdx.z;
-    const int r0 = blockIdx.y * kTile, c0 = blockIdx.x * kTile;
+    const int r0 = blockIdx.y * kTile;
     const int64_t per = (int64_t)rows * cols;
     uint16_t* src = x + (int64_t)g * per;
     uint16_t* dst = xt + (int64_t)g * per;
@@ -117,37 +120,53 @@ __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ 
     }
     const double rd = 1.0 / (double)d;
     const int t = threadIdx.x;
-    {
-        const int r = t >> 2, cc = (t & 3) * 16;  // 16 elements of row r
-        uint16_t* p = src + (int64_t)(r0 + r) * cols + c0 + cc;
+    for (int tt = 0; tt < TPW; ++tt) {
+        const int c0 = (blockIdx.x * TPW + tt) * kTile;
+        {
+            const int r = t >> 2, cc = (t & 3) * 16;  // 16 elements of row r
+            uint16_t* p = src + (int64_t)(r0 + r) * cols + c0 + cc;
+            u32x4 v[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            u32x4 v = *reinterpret_cast<const u32x4*>(p + 8 * h);
+            for (int h = 0; h < 2; ++h) v[h] = *reinterpret_cast<const u32x4*>(p + 8 * h);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float lo = div_by_block(__uint_as_float(v[c] << 16), rd);
-                const float hi = div_by_block(__uint_as_float(v[c] & 0xffff0000u), rd);
-                const uint32_t blo = from_f32<bf16_t>(lo).bits, bhi = from_f32<bf16_t>(hi).bits;
-                v[c] = blo | (bhi << 16);
-                tile[r][cc + 8 * h + 2 * c] = (uint16_t)blo;
-                tile[r][cc + 8 * h + 2 * c + 1] = (uint16_t)bhi;
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float lo = div_by_block(__uint_as_float(v[h][c] << 16), rd);
+                    const float hi = div_by_block(__uint_as_float(v[h][c] & 0xffff0000u), rd);
+                    const uint32_t blo = from_f32<bf16_t>(lo).bits, bhi = from_f32<bf16_t>(hi).bits;
+                    v[h][c] = blo | (bhi << 16);
+                    tile[r][cc + 8 * h + 2 * c] = (uint16_t)blo;
+                    tile[r][cc + 8 * h + 2 * c + 1] = (uint16_t)bhi;
+                }
+                *reinterpret_cast<u32x4*>(p + 8 * h) = v[h];
             }
-            *reinterpret_cast<u32x4*>(p + 8 * h) = v;
         }
-    }
-    __syncthreads();
-    {
-        const int c = t >> 2, rr = (t & 3) * 16;  // 16 elements of column c (row c of x^T)
-        uint16_t* q = dst + (int64_t)(c0 + c) * rows + r0 + rr;
+        __syncthreads();
+        {
+            const int c = t >> 2, rr = (t & 3) * 16;  // 16 elements of column c (row c of x^T)
+            uint16_t* q = dst + (int64_t)(c0 + c) * rows + r0 + rr;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            u32x4 v;
+            for (int h = 0; h < 2; ++h) {
+                u32x4 v;
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                v[k] = (uint32_t)tile[rr + 8 * h + 2 * k][c] | ((uint32_t)tile[rr + 8 * h + 2 * k + 1][c] << 16);
-            *reinterpret_cast<u32x4*>(q + 8 * h) = v;
+                for (int k = 0; k < 4; ++k)
+                    v[k] = (uint32_t)tile[rr + 8 * h + 2 * k][c] | ((uint32_t)tile[rr + 8 * h + 2 * k + 1][c] << 16);
+                *reinterpret_cast<u32x4*>(q + 8 * h) = v;
+            }
         }
+        if (TPW > 1) __syncthreads();  // the tile is rewritten by the next column tile
     }
+}
+
+void launch_scale_transpose(uint16_t* x, uint16_t* xt, int batch, int rows, int cols, const float* div,
+                            const double* sumsq, const int32_t* index, float eps_bf16, hipStream_t st) {
+    if (cols % (2 * kTile) == 0)
+        hipLaunchKernelGGL(k_scale_transpose<2>, dim3(cols / (2 * kTile), rows / kTile, batch), dim3(256), 0, st, x, xt,
+                           rows, cols, div, sumsq, index, eps_bf16);
+    else
+        hipLaunchKernelGGL(k_scale_transpose<1>, dim3(cols / kTile, rows / kTile, batch), dim3(256), 0, st, x, xt,
+                           rows, cols, div, sumsq, index, eps_bf16);
 }
 
 // ---------------------------------------------------------------------------
@@ -240,8 +259,7 @@ extern "C" int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols
         rc = launch_status("gefen_ns_prepare (norm)");
     }
     if (rc == GEFEN_OK) {
-        hipLaunchKernelGGL(muon::k_scale_transpose, dim3(cols / muon::kTile, rows / muon::kTile, batch), dim3(256), 0,
-                           st, X, static_cast<uint16_t*>(xt), rows, cols, div, nullptr, nullptr, 0.0f);
+        muon::launch_scale_transpose(X, static_cast<uint16_t*>(xt), batch, rows, cols, div, nullptr, nullptr, 0.0f, st);
         rc = launch_status("gefen_ns_prepare (scale)");
     }
     (void)hipFreeAsync(ws, st);
@@ -258,9 +276,8 @@ extern "C" int gefen_ns_prepare_sumsq(void* x, void* xt, int batch, int rows, in
     if (!aligned(x, 16) || !aligned(xt, 16)) return fail_inval("gefen_ns_prepare needs 16-byte aligned buffers");
     if (batch > 65535) return fail_inval("batch too large");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(muon::k_scale_transpose, dim3(cols / muon::kTile, rows / muon::kTile, batch), dim3(256), 0, st,
-                       static_cast<uint16_t*>(x), static_cast<uint16_t*>(xt), rows, cols, nullptr, sumsq, index,
-                       muon::eps_to_bf16(eps));
+    muon::launch_scale_transpose(static_cast<uint16_t*>(x), static_cast<uint16_t*>(xt), batch, rows, cols, nullptr,
+                                 sumsq, index, muon::eps_to_bf16(eps), st);
     return launch_status("gefen_ns_prepare_sumsq");
 }
 
