@@ -44,6 +44,7 @@ SIGNATURES = {
     "gefen_muon_tasks_sumsq": (I32, [P, I32, P, P, P]),
     "gefen_ns_prepare": (I32, [P, P, I32, I32, I32, DBL, P]),
     "gefen_ns_prepare_sumsq": (I32, [P, P, I32, I32, I32, DBL, P, P, P]),
+    "gefen_ns_normalize_sumsq": (I32, [P, P, I32, I32, I32, DBL, P, P, I32, P]),
     "gefen_muon_apply_tasks": (I32, [P, I32, P]),
     "gefen_exact_histogram": (I32, [P, I32, I64, I64, P, I32, P]),
     "gefen_accumulate_counts": (I32, [P, P, I32, P]),
@@ -59,6 +60,7 @@ SIGNATURES = {
     "gefen_gemm_bf16": (I32, [P, I64, P, I64, I32, P, I64, P, I64, I32, I32, I32, DBL, DBL, P]),
     "gefen_gemm_bf16_nt_batched": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, I32,
                                          I32, I32, I32, DBL, DBL, I32, P]),
+    "gefen_gram_bf16_batched": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, DBL, P]),
 }
 
 # numpy mirror of struct gefen_step_task / gefen_muon_task (natural C alignment)

@@ -98,7 +98,7 @@ __device__ __forceinline__ float divisor_from_sumsq(double s, float eps_bf16) {
 constexpr int kTile = 64;
 // TPW tiles of one row band per workgroup (the divisor is formed once): two
 // when cols is a multiple of 128 (8% faster on the GefenMuon stacks), else one.
-template <int TPW>
+template <int TPW, bool WRITE_X>
 __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ x, uint16_t* __restrict__ xt,
                                                          int rows, int cols, const float* __restrict__ div,
                                                          const double* __restrict__ sumsq,
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ 
                     tile[r][cc + 8 * h + 2 * c] = (uint16_t)blo;
                     tile[r][cc + 8 * h + 2 * c + 1] = (uint16_t)bhi;
                 }
-                *reinterpret_cast<u32x4*>(p + 8 * h) = v[h];
+                if (WRITE_X) *reinterpret_cast<u32x4*>(p + 8 * h) = v[h];
             }
         }
         __syncthreads();
@@ -159,14 +159,36 @@ __global__ __launch_bounds__(256) void k_scale_transpose(uint16_t* __restrict__ 
     }
 }
 
+template <bool WRITE_X>
 void launch_scale_transpose(uint16_t* x, uint16_t* xt, int batch, int rows, int cols, const float* div,
                             const double* sumsq, const int32_t* index, float eps_bf16, hipStream_t st) {
     if (cols % (2 * kTile) == 0)
-        hipLaunchKernelGGL(k_scale_transpose<2>, dim3(cols / (2 * kTile), rows / kTile, batch), dim3(256), 0, st, x, xt,
-                           rows, cols, div, sumsq, index, eps_bf16);
+        hipLaunchKernelGGL((k_scale_transpose<2, WRITE_X>), dim3(cols / (2 * kTile), rows / kTile, batch), dim3(256), 0,
+                           st, x, xt, rows, cols, div, sumsq, index, eps_bf16);
     else
-        hipLaunchKernelGGL(k_scale_transpose<1>, dim3(cols / kTile, rows / kTile, batch), dim3(256), 0, st, x, xt,
-                           rows, cols, div, sumsq, index, eps_bf16);
+        hipLaunchKernelGGL((k_scale_transpose<1, WRITE_X>), dim3(cols / kTile, rows / kTile, batch), dim3(256), 0, st,
+                           x, xt, rows, cols, div, sumsq, index, eps_bf16);
+}
+
+// x[g] = bf16(x[g] / d_g) in place (d_g from the sums of squares as above):
+// 8 elements per thread, rows * cols a multiple of 2048.
+constexpr int kScaleElems = 256 * 8;
+__global__ __launch_bounds__(256) void k_scale(uint16_t* __restrict__ x, int64_t per, const double* __restrict__ sumsq,
+                                                const int32_t* __restrict__ index, float eps_bf16) {
+    const int g = blockIdx.y;
+    const double* slots = sumsq + (size_t)(index ? index[g] : g) * GEFEN_SUMSQ_STRIDE;
+    double s = 0.0;
+    for (int i = 0; i < GEFEN_SUMSQ_SLOTS; ++i) s += slots[16 * i];
+    const double rd = 1.0 / (double)divisor_from_sumsq(s, eps_bf16);
+    uint16_t* p = x + (int64_t)g * per + (int64_t)blockIdx.x * kScaleElems + 8 * threadIdx.x;
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t lo = from_f32<bf16_t>(div_by_block(__uint_as_float(v[c] << 16), rd)).bits;
+        const uint32_t hi = from_f32<bf16_t>(div_by_block(__uint_as_float(v[c] & 0xffff0000u), rd)).bits;
+        v[c] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(p) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -259,7 +281,8 @@ extern "C" int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols
         rc = launch_status("gefen_ns_prepare (norm)");
     }
     if (rc == GEFEN_OK) {
-        muon::launch_scale_transpose(X, static_cast<uint16_t*>(xt), batch, rows, cols, div, nullptr, nullptr, 0.0f, st);
+        muon::launch_scale_transpose<true>(X, static_cast<uint16_t*>(xt), batch, rows, cols, div, nullptr, nullptr, 0.0f,
+                                           st);
         rc = launch_status("gefen_ns_prepare (scale)");
     }
     (void)hipFreeAsync(ws, st);
@@ -276,9 +299,34 @@ extern "C" int gefen_ns_prepare_sumsq(void* x, void* xt, int batch, int rows, in
     if (!aligned(x, 16) || !aligned(xt, 16)) return fail_inval("gefen_ns_prepare needs 16-byte aligned buffers");
     if (batch > 65535) return fail_inval("batch too large");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    muon::launch_scale_transpose(static_cast<uint16_t*>(x), static_cast<uint16_t*>(xt), batch, rows, cols, nullptr,
-                                 sumsq, index, muon::eps_to_bf16(eps), st);
+    muon::launch_scale_transpose<true>(static_cast<uint16_t*>(x), static_cast<uint16_t*>(xt), batch, rows, cols,
+                                       nullptr, sumsq, index, muon::eps_to_bf16(eps), st);
     return launch_status("gefen_ns_prepare_sumsq");
+}
+
+extern "C" int gefen_ns_normalize_sumsq(void* x, void* out, int batch, int rows, int cols, double eps,
+                                        const double* sumsq, const int32_t* index, int transpose,
+                                        gefen_stream_t stream) {
+    if (batch < 0 || rows < 0 || cols < 0) return fail_inval("negative size");
+    if (batch == 0 || rows == 0 || cols == 0) return GEFEN_OK;
+    if (!x || !sumsq || (transpose && !out)) return fail_inval("null pointer");
+    if (rows % muon::kTile || cols % muon::kTile)
+        return fail_inval("gefen_ns_normalize_sumsq needs rows and cols that are multiples of 64 (got %d, %d)", rows,
+                          cols);
+    if (!aligned(x, 16) || (out && !aligned(out, 16))) return fail_inval("gefen_ns_normalize_sumsq needs 16-byte aligned buffers");
+    if (batch > 65535) return fail_inval("batch too large");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (transpose) {
+        if (out == x) return fail_inval("the transposed output cannot overwrite its input");
+        muon::launch_scale_transpose<false>(static_cast<uint16_t*>(x), static_cast<uint16_t*>(out), batch, rows, cols,
+                                            nullptr, sumsq, index, muon::eps_to_bf16(eps), st);
+    } else {
+        if (out && out != x) return fail_inval("the normalisation without transpose is in place (out must be x or null)");
+        const int64_t per = (int64_t)rows * cols;  // a multiple of 4096
+        hipLaunchKernelGGL(muon::k_scale, dim3((unsigned)(per / muon::kScaleElems), batch), dim3(256), 0, st,
+                           static_cast<uint16_t*>(x), per, sumsq, index, muon::eps_to_bf16(eps));
+    }
+    return launch_status("gefen_ns_normalize_sumsq");
 }
 
 extern "C" int gefen_muon_apply_tasks(const gefen_muon_apply_task* tasks, int ntasks, gefen_stream_t stream) {

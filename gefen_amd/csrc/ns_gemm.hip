@@ -15,6 +15,7 @@
 // LDS read.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "capi_internal.h"
 #include "common.h"
@@ -254,6 +255,50 @@ __device__ __forceinline__ void tile_store(uint16_t* lds, const u32x4 in[TCH]) {
     }
 }
 
+// MN-major operand (the Gram product X X^T with only X^T stored): the operand is
+// given as its transpose [K, 256-column block], and a K step of the tile is
+// rows k0 .. k0 + TK of it, 256 elements each.  LDS keeps that layout, [k][m]
+// in rows of TLDM elements (576 bytes: consecutive rows start 16 banks apart,
+// so the transposed fragment reads below are conflict-free), and fragments come
+// out of ds_read_b64_tr_b16.  Chunk q = threadIdx.x + TT i is row q / MCPR,
+// column chunk q % MCPR; chunk i is TT / MCPR rows on.
+constexpr int MCPR = TM / 8;   // 16-byte chunks per K row of the tile
+constexpr int TLDM = TM + 32;  // LDS row of an MN-major stage (bf16)
+static_assert(TK * TLDM == TM * TLD, "an MN-major stage has the size of a K-major one");
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc_mn(const uint16_t* cols, int64_t ld, int K) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(cols), (short)0, (int)(K * ld * 2), 0x00020000);
+}
+__device__ __forceinline__ void tile_load_mn(__amdgpu_buffer_rsrc_t rs, int voff, int64_t ld, int k0, u32x4 out[TCH]) {
+#pragma unroll
+    for (int i = 0; i < TCH; ++i)
+        out[i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, (int)(((int64_t)(TT / MCPR) * i + k0) * ld * 2), 0));
+}
+__device__ __forceinline__ void tile_store_mn(uint16_t* lds, const u32x4 in[TCH]) {
+#pragma unroll
+    for (int i = 0; i < TCH; ++i) {
+        const int q = threadIdx.x + TT * i;
+        *reinterpret_cast<u32x4*>(lds + (q / MCPR) * TLDM + (q % MCPR) * 8) = in[i];
+    }
+}
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane 4 j + q gives the address
+// of 4 elements (row j, columns 4 q .. 4 q + 3 of a 4 x 16 block) and lane i
+// receives column i, rows 0 .. 3.  The MFMA operand of lane l (row l % 32, k =
+// 8 (l / 32) + 0..7) is two such reads: lane l points at K row kk + 8 (l / 32) +
+// (l % 16) / 4 (+ 4 for the second read), column 16 ((l / 16) % 2) + 4 (l % 4).
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int mn_lane_offset(int lane) {
+    const int g = lane >> 4, r = lane & 15;
+    return (8 * (g >> 1) + (r >> 2)) * TLDM + 16 * (g & 1) + 4 * (r & 3);
+}
+__device__ __forceinline__ bf16x8 mn_frag(const uint16_t* p) {
+    typedef __attribute__((address_space(3))) bf16x4 lds_v4;
+    const auto* q = (const __attribute__((address_space(3))) uint16_t*)p;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4*)q);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4*)(q + 4 * TLDM));
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 #ifndef GEFEN_NS_XCD
 #define GEFEN_NS_XCD 1
 #endif
@@ -286,6 +331,8 @@ constexpr int LDT = TM + 4;
 static_assert(TM == TN, "square tiles");
 static_assert(TN * LDT <= 4 * TM * TLD, "the epilogue tile fits in the operand stages");
 
+// MN: both operands MN-major (the symmetric Gram product from X^T; no D, no C^T).
+template <bool MN>
 __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     // operand stages: A in [0, 2) and B in [2, 4) of TM x TLD each; the epilogue reuses them
     __shared__ __attribute__((aligned(16))) uint16_t smem[4 * TM * TLD];
@@ -325,18 +372,34 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
 
     const int nk = g.K / TK;
     u32x4 ra[TCH], rb[TCH];  // register stage of the global -> LDS pipeline
-    const __amdgpu_buffer_rsrc_t rsa = tile_rsrc(A + (int64_t)m0 * g.lda, g.lda);
-    const __amdgpu_buffer_rsrc_t rsb = tile_rsrc(B + (int64_t)n0 * g.ldb, g.ldb);
-    const int voa = (int)(((threadIdx.x / CPR) * g.lda + (threadIdx.x % CPR) * 8) * 2);
-    const int vob = (int)(((threadIdx.x / CPR) * g.ldb + (threadIdx.x % CPR) * 8) * 2);
-    tile_load(rsa, voa, g.lda, 0, ra);
-    tile_load(rsb, vob, g.ldb, 0, rb);
-    tile_store(As[0], ra);
-    tile_store(Bs[0], rb);
-    if (nk > 1) {
-        tile_load(rsa, voa, g.lda, TK, ra);
-        tile_load(rsb, vob, g.ldb, TK, rb);
-    }
+    const __amdgpu_buffer_rsrc_t rsa = MN ? tile_rsrc_mn(A + m0, g.lda, g.K) : tile_rsrc(A + (int64_t)m0 * g.lda, g.lda);
+    const __amdgpu_buffer_rsrc_t rsb = MN ? tile_rsrc_mn(B + n0, g.ldb, g.K) : tile_rsrc(B + (int64_t)n0 * g.ldb, g.ldb);
+    const int voa = MN ? (int)(((threadIdx.x / MCPR) * g.lda + (threadIdx.x % MCPR) * 8) * 2)
+                       : (int)(((threadIdx.x / CPR) * g.lda + (threadIdx.x % CPR) * 8) * 2);
+    const int vob = MN ? (int)(((threadIdx.x / MCPR) * g.ldb + (threadIdx.x % MCPR) * 8) * 2)
+                       : (int)(((threadIdx.x / CPR) * g.ldb + (threadIdx.x % CPR) * 8) * 2);
+    auto load_ops = [&](int k0) {
+        if (MN) {
+            tile_load_mn(rsa, voa, g.lda, k0, ra);
+            tile_load_mn(rsb, vob, g.ldb, k0, rb);
+        } else {
+            tile_load(rsa, voa, g.lda, k0, ra);
+            tile_load(rsb, vob, g.ldb, k0, rb);
+        }
+    };
+    auto store_ops = [&](int stage) {
+        if (MN) {
+            tile_store_mn(As[stage], ra);
+            tile_store_mn(Bs[stage], rb);
+        } else {
+            tile_store(As[stage], ra);
+            tile_store(Bs[stage], rb);
+        }
+    };
+    const int mn_lofs = MN ? mn_lane_offset(lane) : 0;
+    load_ops(0);
+    store_ops(0);
+    if (nk > 1) load_ops(TK);
     __syncthreads();
     // One K step from LDS stage CUR.  It first stores step kt + 1 (loaded during
     // step kt - 1) into the other LDS stage, which every wave finished reading
@@ -351,10 +414,15 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     // MFMAs, measured 5% slower: the stores then wait at the end of every step.)
 #define GEFEN_LOAD_FRAGS(AS, BS, KK, AF, BF)                                                                      \
     {                                                                                                             \
+    if (MN) {                                                                                                     \
+        _Pragma("unroll") for (int i = 0; i < WI; ++i) AF[i] = mn_frag((AS) + (KK) * TLDM + mn_lofs + wm + i * 32); \
+        _Pragma("unroll") for (int j = 0; j < WJ; ++j) BF[j] = mn_frag((BS) + (KK) * TLDM + mn_lofs + wn + j * 32); \
+    } else {                                                                                                      \
         _Pragma("unroll") for (int i = 0; i < WI; ++i) AF[i] =                                                    \
             *reinterpret_cast<const bf16x8*>((AS) + (wm + i * 32 + (lane & 31)) * TLD + (KK) + 8 * (lane >> 5));  \
         _Pragma("unroll") for (int j = 0; j < WJ; ++j) BF[j] =                                                    \
             *reinterpret_cast<const bf16x8*>((BS) + (wn + j * 32 + (lane & 31)) * TLD + (KK) + 8 * (lane >> 5));  \
+    }                                                                                                             \
     }
 #define GEFEN_MFMAS(AF, BF)                                                                                       \
     _Pragma("unroll") for (int i = 0; i < WI; ++i) _Pragma("unroll") for (int j = 0; j < WJ; ++j) acc[i][j] =     \
@@ -362,24 +430,19 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     // instruction groups in issue order (masks: 0x008 MFMA, 0x100 LDS read, 0x020 global read)
 #define GEFEN_SCHED_STEP                                                                                          \
     {                                                                                                             \
-        __builtin_amdgcn_sched_group_barrier(0x100, WI + WJ, 0);                                                  \
+        __builtin_amdgcn_sched_group_barrier(0x100, (WI + WJ) * (MN ? 2 : 1), 0);                                 \
         _Pragma("unroll") for (int s_ = 0; s_ < TK / 16; ++s_) {                                                  \
             _Pragma("unroll") for (int t_ = 0; t_ < WI * WJ; ++t_) {                                              \
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                \
-                if (s_ + 1 < TK / 16 && t_ < WI + WJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          \
+                if (s_ + 1 < TK / 16 && t_ < WI + WJ) __builtin_amdgcn_sched_group_barrier(0x100, MN ? 2 : 1, 0); \
                 if (s_ == 0 && t_ < 2 * TCH) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                   \
             }                                                                                                     \
         }                                                                                                         \
     }
 #define GEFEN_TILE_STEP(KT, CUR)                                                                                  \
     {                                                                                                             \
-        if ((KT) + 1 < nk) {                                                                                      \
-            tile_store(As[(CUR) ^ 1], ra);                                                                        \
-            tile_store(Bs[(CUR) ^ 1], rb);                                                                        \
-        }                                                                                                         \
-        const int kpre = min((KT) + 2, nk - 1) * TK;                                                              \
-        tile_load(rsa, voa, g.lda, kpre, ra);                                                                     \
-        tile_load(rsb, vob, g.ldb, kpre, rb);                                                                     \
+        if ((KT) + 1 < nk) store_ops((CUR) ^ 1);                                                                  \
+        load_ops(min((KT) + 2, nk - 1) * TK);                                                                     \
         const uint16_t* as = As[CUR];                                                                             \
         const uint16_t* bs = Bs[CUR];                                                                             \
         bf16x8 af0[WI], bf0[WJ], af1[WI], bf1[WJ];                                                                \
@@ -409,7 +472,7 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
     // C^T (CT, or the mirror tile of a symmetric product), and C's rows are
     // gathered from two column chunks per wave instruction.  D given as D^T is
     // staged through T the same way; a row-major D is read directly.
-    uint16_t* __restrict__ C = g.C + batch * g.sc;
+    uint16_t* __restrict__ C = g.C ? g.C + batch * g.sc : nullptr;
     uint16_t* __restrict__ CT = g.CT ? g.CT + batch * g.sct : nullptr;
     const uint16_t* __restrict__ D = g.D ? g.D + batch * g.sd : nullptr;
     const bool mirror = g.symmetric && ti != tj;
@@ -485,7 +548,8 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
         }
     }
     // rows of C: lanes 0-31 take 32 consecutive rows of column chunk k, lanes
-    // 32-63 the same rows of chunk k + 1
+    // 32-63 the same rows of chunk k + 1 (C may be absent when only C^T is wanted)
+    if (!g.C) return;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
         const int q = threadIdx.x + TT * i;
@@ -540,8 +604,9 @@ extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t st
                                           double alpha, double beta, int symmetric, gefen_stream_t stream) {
     if (m < 0 || n < 0 || k < 0 || batch < 0) return fail_inval("negative GEMM size");
     if (m == 0 || n == 0 || batch == 0) return GEFEN_OK;
-    if (!a || !b || !c || (beta != 0.0 && !d)) return fail_inval("null GEMM operand");
-    if (lda < k || ldb < k || ldc < n || (ct && ldct < m) || (d && ldd < (d_transposed ? m : n)))
+    if (!a || !b || (!c && !ct) || (beta != 0.0 && !d)) return fail_inval("null GEMM operand");
+    if (!c && symmetric) return fail_inval("a symmetric GEMM needs C");
+    if (lda < k || ldb < k || (c && ldc < n) || (ct && ldct < m) || (d && ldd < (d_transposed ? m : n)))
         return fail_inval("GEMM leading dimension too small");
     if (symmetric && m != n) return fail_inval("a symmetric GEMM must be square");
     if (symmetric && ct) return fail_inval("a symmetric GEMM has no separate transposed output (C^T = C)");
@@ -575,6 +640,43 @@ extern "C" int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t st
     if (g.D && d_transposed && ldd % 4) return fail_inval("D^T rows must be 8-byte aligned");
     const int64_t grid = (int64_t)g.tiles * batch;
     if (grid > INT32_MAX) return fail_inval("batched GEMM grid too large");
-    hipLaunchKernelGGL(ns::k_gemm_tile, dim3((unsigned)grid), dim3(ns::TT), 0, reinterpret_cast<hipStream_t>(stream), g);
+    hipLaunchKernelGGL(ns::k_gemm_tile<false>, dim3((unsigned)grid), dim3(ns::TT), 0, reinterpret_cast<hipStream_t>(stream),
+                       g);
     return launch_status("gefen_gemm_bf16_nt_batched");
+}
+
+extern "C" int gefen_gram_bf16_batched(const void* xt, int64_t ldxt, int64_t stride_xt, void* c, int64_t ldc,
+                                       int64_t stride_c, int batch, int m, int k, double alpha,
+                                       gefen_stream_t stream) {
+    if (m < 0 || k < 0 || batch < 0) return fail_inval("negative GEMM size");
+    if (m == 0 || batch == 0) return GEFEN_OK;
+    if (!xt || !c) return fail_inval("null GEMM operand");
+    if (ldxt < m || ldc < m) return fail_inval("GEMM leading dimension too small");
+    if (m % ns::TM || k % ns::TK || k == 0)
+        return fail_inval("batched Gram product needs m a multiple of 256 and k a multiple of %d (got %d, %d)", ns::TK,
+                          m, k);
+    if ((int64_t)k * ldxt * 2 > INT32_MAX)
+        return fail_inval("batched Gram product operand too large (k rows must span less than 2^31 bytes)");
+    if (!aligned(xt, 16) || !aligned(c, 16) || ldxt % 8 || ldc % 8 || stride_xt % 8 || stride_c % 8)
+        return fail_inval("batched GEMM operands need 16-byte aligned rows");
+    ns::TileGemm g;
+    memset(&g, 0, sizeof(g));
+    g.A = g.B = static_cast<const uint16_t*>(xt);
+    g.C = static_cast<uint16_t*>(c);
+    g.lda = g.ldb = ldxt;
+    g.ldc = ldc;
+    g.sa = g.sb = stride_xt;
+    g.sc = stride_c;
+    g.M = g.N = m;
+    g.K = k;
+    g.alpha = (float)alpha;
+    g.beta = 0.0f;
+    g.tiles_n = m / ns::TN;
+    g.symmetric = 1;
+    g.tiles = g.tiles_n * (g.tiles_n + 1) / 2;
+    const int64_t grid = (int64_t)g.tiles * batch;
+    if (grid > INT32_MAX) return fail_inval("batched GEMM grid too large");
+    hipLaunchKernelGGL(ns::k_gemm_tile<true>, dim3((unsigned)grid), dim3(ns::TT), 0, reinterpret_cast<hipStream_t>(stream),
+                       g);
+    return launch_status("gefen_gram_bf16_batched");
 }

@@ -5,9 +5,11 @@ times:  A = X X^T;  B = b A + c A A;  X = a X + B X.  Each product rounds
 alpha*AB + beta*D to bf16 once, as torch.addmm does.
 
 newton_schulz_batched runs a stack of same-shaped matrices at once with the
-large-tile batched GEMM (every product in A B^T form: X X^T, A A with A
-symmetric, B X from X^T, which each step writes beside X); newton_schulz_bf16
-is the one-matrix path for shapes the batched GEMM does not tile.
+large-tile batched GEMM, keeping only X^T between iterations: X X^T comes from
+X^T through transposing LDS reads (gefen_gram_bf16_batched), b A + c A A is an
+A B^T product of the symmetric A, and B X = (X^T B)^T is written as X'^T (the
+last iteration writes the orientation it returns).  newton_schulz_bf16 is the
+one-matrix path for shapes the batched GEMM does not tile.
 """
 
 from __future__ import annotations
@@ -65,7 +67,8 @@ def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: 
                     d: torch.Tensor = None, alpha: float = 1.0, beta: float = 0.0, symmetric: bool = False,
                     d_t: torch.Tensor = None) -> None:
     """out[i] = alpha * a[i] @ b[i]^T + beta * D[i] (and out_t[i] = out[i]^T) for stacked bf16
-    matrices; D is given as d, or as its transpose d_t (read four rows at a time)."""
+    matrices; D is given as d, or as its transpose d_t (read four rows at a time); out may be
+    None when out_t is given (only the transposed result is written)."""
     if d is not None and d_t is not None:
         raise ValueError("give D as d or as d_t, not both")
     transposed_d = d_t is not None
@@ -85,18 +88,27 @@ def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: 
         return t.stride(0) if t is not None else 0
 
     rc = lib.gefen_gemm_bf16_nt_batched(a.data_ptr(), a.stride(1), a.stride(0), b.data_ptr(), b.stride(1), b.stride(0),
-                                        out.data_ptr(), out.stride(1), out.stride(0), ptr(out_t), ld(out_t), bs(out_t),
+                                        ptr(out), ld(out), bs(out), ptr(out_t), ld(out_t), bs(out_t),
                                         ptr(d), ld(d), bs(d), 1 if transposed_d else 0, g, m, n, k, float(alpha),
                                         float(beta), 1 if symmetric else 0,
                                         torch.cuda.current_stream(a.device).cuda_stream)
     _lib.check(rc, "gefen_gemm_bf16_nt_batched")
 
 
+def gram_batched(xt: torch.Tensor, out: torch.Tensor) -> None:
+    """out[i] = X[i] @ X[i]^T for the stacked X[i]^T = xt[i] ([k, m] bf16, row-major)."""
+    g, k, m = xt.shape
+    lib = _lib.load()
+    rc = lib.gefen_gram_bf16_batched(xt.data_ptr(), xt.stride(1), xt.stride(0), out.data_ptr(), out.stride(1),
+                                     out.stride(0), g, m, k, 1.0, torch.cuda.current_stream(xt.device).cuda_stream)
+    _lib.check(rc, "gefen_gram_bf16_batched")
+
+
 def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], steps: int,
                           eps: float, work: Optional[dict] = None, sumsq: Optional[torch.Tensor] = None,
                           index: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Newton-Schulz of every matrix of a [G, rows, cols] bf16 stack, in place of
-    x's values (x is normalised in place); returns the [G, rows, cols] result.
+    """Newton-Schulz of every matrix of a [G, rows, cols] bf16 stack; returns the
+    [G, rows, cols] result.  x's values may be overwritten.
 
     work: a dict that keeps the intermediate buffers between calls with the same
     stack (allocated on first use); the result is then the same buffer on every
@@ -107,6 +119,7 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
     a, b, c = coeffs
     g, rows, cols = x.shape
     transposed = rows > cols
+    m, n = (cols, rows) if transposed else (rows, cols)  # X [m, n], m <= n
     if work is None:
         work = {}
 
@@ -116,37 +129,40 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
             t = work[name] = torch.empty(shape, dtype=torch.bfloat16, device=x.device)
         return t
 
-    # normalise each matrix, x /= max(||x||, eps) in bf16 (gefen_muon.py:37), and
-    # write its transpose: X [G, m, n] with m <= n and X^T
-    other = buf("other", (g, cols, rows))
+    # normalise each matrix, x /= max(||x||, eps) in bf16 (gefen_muon.py:37), as
+    # X^T [G, n, m]: the stack itself for a transposed stack, its transpose else
     lib = _lib.load()
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream(x.device).cuda_stream
         if sumsq is not None:
-            _lib.check(lib.gefen_ns_prepare_sumsq(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps),
-                                                  sumsq.data_ptr(), index.data_ptr() if index is not None else None,
-                                                  stream), "gefen_ns_prepare_sumsq")
+            xt = x if transposed else buf("xt", (g, n, m))
+            _lib.check(lib.gefen_ns_normalize_sumsq(x.data_ptr(), None if transposed else xt.data_ptr(), g, rows, cols,
+                                                    float(eps), sumsq.data_ptr(),
+                                                    index.data_ptr() if index is not None else None,
+                                                    0 if transposed else 1, stream), "gefen_ns_normalize_sumsq")
         else:
+            other = buf("other", (g, cols, rows))
             _lib.check(lib.gefen_ns_prepare(x.data_ptr(), other.data_ptr(), g, rows, cols, float(eps), stream),
                        "gefen_ns_prepare")
-    x, xt = (other, x) if transposed else (x, other)
-    m, n = x.shape[1], x.shape[2]
+            xt = x if transposed else other
+    if steps == 0:
+        if transposed:
+            return xt
+        out = buf("nx", (g, m, n))
+        out.copy_(xt.transpose(1, 2))
+        return out
     gram = buf("gram", (g, m, m))
     upd = buf("upd", (g, m, m))
-    nx, nxt = buf("nx", (g, m, n)), buf("nxt", (g, n, m))
+    nxt = buf("t1", (g, n, m))  # X^T alternates between xt and this buffer
     with torch.cuda.device(x.device):
         for it in range(steps):
-            gemm_nt_batched(x, x, gram, symmetric=True)                                # X X^T
-            gemm_nt_batched(gram, gram, upd, d_t=gram, alpha=c, beta=b, symmetric=True)  # b A + c A A
-            if it + 1 < steps:
-                gemm_nt_batched(upd, xt, nx, out_t=nxt, d_t=xt, alpha=1.0, beta=a)       # a X + B X (and ^T)
-                x, nx = nx, x
+            gram_batched(xt, gram)                                                        # X X^T
+            gemm_nt_batched(gram, gram, upd, d_t=gram, alpha=c, beta=b, symmetric=True)   # b A + c A A
+            if it + 1 < steps or transposed:
+                gemm_nt_batched(upd, xt, None, out_t=nxt, d_t=xt, alpha=1.0, beta=a)      # (a X + B X)^T
                 xt, nxt = nxt, xt
-            elif transposed:
-                # last step, result wanted as X^T: a X^T + X^T B with B symmetric
-                gemm_nt_batched(xt, upd, nxt, d_t=x, alpha=1.0, beta=a)
-                xt = nxt
             else:
-                gemm_nt_batched(upd, xt, nx, d_t=xt, alpha=1.0, beta=a)
-                x = nx
-    return xt if transposed else x
+                nx = buf("nx", (g, m, n))
+                gemm_nt_batched(upd, xt, nx, d_t=xt, alpha=1.0, beta=a)                   # a X + B X
+                return nx
+    return xt

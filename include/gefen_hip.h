@@ -194,6 +194,13 @@ int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols, double ep
 int gefen_ns_prepare_sumsq(void* x, void* xt, int batch, int rows, int cols, double eps, const double* sumsq,
                            const int32_t* index, gefen_stream_t stream);
 
+/* The same normalisation written in one orientation only: transpose = 1,
+ * out[g] = (x[g] / max(bf16(||x[g]||), bf16(eps)))^T [cols, rows], x unchanged;
+ * transpose = 0, x[g] normalised in place (out NULL or x).  The norms come
+ * from the partial sums as in gefen_ns_prepare_sumsq. */
+int gefen_ns_normalize_sumsq(void* x, void* out, int batch, int rows, int cols, double eps, const double* sumsq,
+                             const int32_t* index, int transpose, gefen_stream_t stream);
+
 /* Replaces the parameter update of gefen_muon.py:325-329 (p.mul_(1 - lr*wd);
  * p.add_(update, alpha=-lr_adj)) with the reference's CPU rounding: reduced
  * dtypes round alpha to the dtype, and round the product first when the
@@ -297,14 +304,24 @@ int gefen_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int 
  * Newton-Schulz keeps X^T beside X).  symmetric = 1 declares C_b symmetric
  * (m == n, e.g. X X^T, or
  * b A + c A A for a symmetric A): only tiles on and above the diagonal are
- * computed and mirrored (ct must then be NULL: C^T = C).  m and n must be
- * multiples of 256, k a multiple of 64,
+ * computed and mirrored (ct must then be NULL: C^T = C).  c may be NULL for a
+ * non-symmetric product when ct is given (only C^T is written).  m and n must
+ * be multiples of 256, k a multiple of 64,
  * rows 16-byte aligned (else ValueError; gefen_gemm_bf16 takes any shape). */
 int gefen_gemm_bf16_nt_batched(const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
                                int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, void* ct,
                                int64_t ldct, int64_t stride_ct, const void* d, int64_t ldd, int64_t stride_d,
                                int d_transposed, int batch, int m, int n, int k, double alpha, double beta,
                                int symmetric, gefen_stream_t stream);
+
+/* The Gram product of Newton-Schulz (A = X @ X.T, gefen_muon.py:41) from X^T
+ * alone: for b < batch, C_b = bf16(alpha * X_b @ X_b^T) [m, m], with X_b^T given
+ * row-major [k, m] (row stride ldxt, matrix stride stride_xt); the result is
+ * bit-identical to gefen_gemm_bf16_nt_batched(X, X, symmetric = 1), so
+ * Newton-Schulz keeps only X^T between iterations.  m a multiple of 256, k of
+ * 64, k * ldxt * 2 < 2^31, rows 16-byte aligned (else ValueError). */
+int gefen_gram_bf16_batched(const void* xt, int64_t ldxt, int64_t stride_xt, void* c, int64_t ldc,
+                            int64_t stride_c, int batch, int m, int k, double alpha, gefen_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -164,3 +164,73 @@ def test_batched_newton_schulz_matches_one_matrix_path(g, rows, cols):
         gi = got[i].float().cpu().numpy()
         rel = np.linalg.norm(gi - ref) / np.linalg.norm(ref)
         assert rel < 2e-2, (i, rel)
+
+
+@pytest.mark.parametrize("g,m,k", [(3, 256, 512), (2, 512, 256), (2, 768, 1024), (1, 256, 64)])
+def test_gram_from_transpose_equals_symmetric_product(g, m, k):
+    """gefen_gram_bf16_batched(X^T) equals gefen_gemm_bf16_nt_batched(X, X,
+    symmetric) bit for bit: the transposing LDS reads build the same MFMA
+    operands in the same K order."""
+    from gefen_amd.newton_schulz import gemm_nt_batched, gram_batched
+
+    gen = torch.Generator(device="cpu").manual_seed(m + 7 * k + g)
+    x = (torch.randn(g, m, k, generator=gen) * 0.05).bfloat16().cuda()
+    xt = x.transpose(1, 2).contiguous()
+    ref = torch.empty(g, m, m, dtype=torch.bfloat16, device="cuda:0")
+    got = torch.empty_like(ref)
+    gemm_nt_batched(x, x, ref, symmetric=True)
+    gram_batched(xt, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def _newton_schulz_both_orientations(x, coeffs, steps, sumsq, index):
+    """The scheme that kept X and X^T (normalisation writes both; B X writes both),
+    composed from gefen_ns_prepare_sumsq and gefen_gemm_bf16_nt_batched."""
+    from gefen_amd import _lib
+    from gefen_amd.newton_schulz import gemm_nt_batched
+
+    a, b, c = coeffs
+    g, rows, cols = x.shape
+    transposed = rows > cols
+    other = torch.empty(g, cols, rows, dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    _lib.check(lib.gefen_ns_prepare_sumsq(x.data_ptr(), other.data_ptr(), g, rows, cols, 1e-7, sumsq.data_ptr(),
+                                          index.data_ptr() if index is not None else None,
+                                          torch.cuda.current_stream().cuda_stream))
+    X, XT = (other, x) if transposed else (x, other)
+    m, n = X.shape[1], X.shape[2]
+    for _ in range(steps):
+        gram = torch.empty(g, m, m, dtype=torch.bfloat16, device=x.device)
+        upd = torch.empty_like(gram)
+        gemm_nt_batched(X, X, gram, symmetric=True)
+        gemm_nt_batched(gram, gram, upd, d_t=gram, alpha=c, beta=b, symmetric=True)
+        nx = torch.empty(g, m, n, dtype=torch.bfloat16, device=x.device)
+        nxt = torch.empty(g, n, m, dtype=torch.bfloat16, device=x.device)
+        gemm_nt_batched(upd, XT, nx, out_t=nxt, d_t=XT, alpha=1.0, beta=a)
+        X, XT = nx, nxt
+    return XT if transposed else X
+
+
+@pytest.mark.parametrize("g,rows,cols", [(3, 256, 512), (2, 512, 256), (2, 512, 768), (2, 768, 256)])
+@pytest.mark.parametrize("steps", [0, 1, 2, 5])
+def test_batched_newton_schulz_keeps_only_the_transpose_bit_exactly(g, rows, cols, steps):
+    """newton_schulz_batched (X^T only between iterations, Gram product from X^T,
+    normalisation in one orientation) equals the scheme that kept both
+    orientations, bit for bit, for transposed and untransposed stacks and even
+    and odd step counts."""
+    from gefen_amd.newton_schulz import newton_schulz_batched
+
+    gen = torch.Generator(device="cpu").manual_seed(rows * 5 + cols + steps)
+    x0 = (torch.randn(g, rows, cols, generator=gen) * 1e-3).bfloat16().cuda()
+    sumsq = torch.zeros(g * 128, dtype=torch.float64, device="cuda:0")
+    sumsq.view(g, 8, 16)[:, 0, 0] = (x0.double() ** 2).sum(dim=(1, 2))
+    index = torch.arange(g - 1, -1, -1, dtype=torch.int32, device="cuda:0")  # matrix i's sums are task g-1-i's
+    sumsq_perm = torch.zeros_like(sumsq)
+    sumsq_perm.view(g, 8, 16)[:, 0, 0] = sumsq.view(g, 8, 16)[:, 0, 0].flip(0)
+    coeffs = (3.4445, -4.7750, 2.0315)
+    ref = _newton_schulz_both_orientations(x0.clone(), coeffs, steps, sumsq, None)
+    got = newton_schulz_batched(x0.clone(), coeffs, steps, 1e-7, sumsq=sumsq_perm, index=index)
+    torch.cuda.synchronize()
+    assert got.shape == ref.shape == x0.shape
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
