@@ -91,7 +91,8 @@ __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restric
     for (int i = t; i < kNb16Bytes; i += 256) {
         uint8_t c = 0;
         if (i < 2 * (int)kNb16Side) {
-            const uint32_t bits = (i < (int)kNb16Side ? 0u : 0x8000u) | (kNb16Lo + (uint32_t)i % kNb16Side);
+            const uint32_t bits = i >= (int)kNb16Side ? kNb16Lo + (uint32_t)(i - (int)kNb16Side)
+                                                      : 0x8000u | (kNb16Lo + kNb16Side - 1u - (uint32_t)i);
             const float x = __uint_as_float(bits << 16);
             int lo = 1, hi = K;  // first k in [1, K) with thr[k] >= x
             while (lo < hi) {

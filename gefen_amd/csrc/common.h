@@ -151,8 +151,10 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 //   bucket8  the same counts as bytes (every count is <= 255), padded with zeros
 //            to 4112 entries: the compact copy the step kernels keep in LDS.
 //   nb16[i]  the nearest index of the bf16 value with bits kNb16Lo + i (i < kNb16Side)
-//            and of its negative (entry kNb16Side + i): every bf16 x with
-//            2^-20 <= |x| <= 1.0078125, the range of the GefenMuon quotients.
+//            at entry kNb16Side + i, and of its negative at entry kNb16Side - 1 - i
+//            (so the entry is kNb16Side + (i ^ s) with s = 0 or -1 from the sign
+//            bit): every bf16 x with 2^-20 <= |x| <= 1.0078125, the range of the
+//            GefenMuon quotients.
 constexpr uint32_t kNb16Lo = 0x3580u;                 // 2^-20
 constexpr uint32_t kNb16Side = 0x3F82u - kNb16Lo;     // up to 0x3F81 = 1.0078125
 constexpr int kNb16Bytes = (2 * kNb16Side + 15) / 16 * 16;

@@ -623,8 +623,41 @@ __device__ __forceinline__ void add_sumsq(float v, double* sumsq, int64_t key) {
 template <typename D>
 __device__ __forceinline__ float muon_blend(float a, float gf, const MuonTask& T) {
     if (!T.nesterov) return a;
-    if (sizeof(D) == 4) return __builtin_fmaf(gf, T.alpha, a);  // fp32: fma
-    return a + gf * T.alpha;  // reduced dtype: alpha in D, exact product, one rounding
+    // fp32: fma; reduced dtype: alpha is in D, so the product is exact and the
+    // fma rounds once, as the unfused sum would
+    return __builtin_fmaf(gf, T.alpha, a);
+}
+
+// bf16 bits of two floats (round to nearest even), a in the low half: one
+// v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t pk_bf16_bits(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 v = __builtin_convertvector((f2){a, b}, b2);
+    uint32_t r;
+    __builtin_memcpy(&r, &v, 4);
+    return r;
+}
+
+// Per-half unsigned max of two packed 16-bit values (v_pk_max_u16).
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+    typedef unsigned short u2 __attribute__((ext_vector_type(2)));
+    u2 x, y;
+    __builtin_memcpy(&x, &a, 4);
+    __builtin_memcpy(&y, &b, 4);
+    const u2 r = __builtin_elementwise_max(x, y);
+    uint32_t o;
+    __builtin_memcpy(&o, &r, 4);
+    return o;
+}
+
+// acc + lo^2 + hi^2 of the two bf16 values packed in v (v_dot2c_f32_bf16; the
+// products are exact in float32).
+__device__ __forceinline__ float dot2_bf16(uint32_t v, float acc) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    b2 x;
+    __builtin_memcpy(&x, &v, 4);
+    return __builtin_amdgcn_fdot2_f32_bf16(x, x, acc, false);
 }
 
 template <typename D, typename S>
@@ -643,6 +676,7 @@ __device__ __forceinline__ float muon_out(float q, float gf, const MuonTask& T) 
 template <typename D, typename S, int W, int R, bool TAB>
 __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     constexpr bool kNb = std::is_same<D, bf16_t>::value;  // bf16 quotients: the nb16 table
+    constexpr bool kPk = kNb && W % 2 == 0;                // bf16 pairs: packed conversions
     __shared__ LdsTables L;
     __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
     __shared__ __attribute__((aligned(16))) uint8_t nb16[kNb ? kNb16Bytes : 16];
@@ -697,19 +731,48 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         float mu[R][W];
-        float mx = 0.0f;
+        uint32_t mxk = 0;  // ordered |m1|: the unsigned max is the NaN-propagating absmax
+        if constexpr (kPk) {
+            // bf16 pairs: one conversion rounds two lerps, and the absmax runs on
+            // the packed |bf16| bits (the top halves of the float32 keys)
+            uint32_t mx2 = 0;
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
+            for (int j = 0; j < R; ++j) {
 #pragma unroll
-            for (int w = 0; w < W; ++w) {
-                const float gf = to_f32(gv[j].v[w]);
-                const float m0 = TAB ? ctab[iv[j].v[w]] : round_to<D>(L.cbd[iv[j].v[w]] * mold);  // dequant * mag
-                const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));                   // lerp_
-                mu[j][w] = m1;
-                mx = nanmax(mx, fabsf(m1));
+                for (int w = 0; w < W; w += 2) {
+                    const float g0 = to_f32(gv[j].v[w]), g1 = to_f32(gv[j].v[w + 1]);
+                    float c0, c1;  // dequant * mag
+                    if (TAB) {
+                        c0 = ctab[iv[j].v[w]];
+                        c1 = ctab[iv[j].v[w + 1]];
+                    } else {
+                        const uint32_t c = pk_bf16_bits(L.cbd[iv[j].v[w]] * mold, L.cbd[iv[j].v[w + 1]] * mold);
+                        c0 = __uint_as_float(c << 16);
+                        c1 = __uint_as_float(c & 0xffff0000u);
+                    }
+                    const uint32_t pk = pk_bf16_bits(__builtin_fmaf(T.w, g0 - c0, c0), __builtin_fmaf(T.w, g1 - c1, c1));
+                    mu[j][w] = __uint_as_float(pk << 16);
+                    mu[j][w + 1] = __uint_as_float(pk & 0xffff0000u);
+                    mx2 = max_u16x2(mx2, pk & 0x7fff7fffu);
+                }
+            }
+            const uint32_t lo = mx2 & 0xffffu, hi = mx2 >> 16;
+            mxk = (lo > hi ? lo : hi) << 16;
+        } else {
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const float gf = to_f32(gv[j].v[w]);
+                    const float m0 = TAB ? ctab[iv[j].v[w]] : round_to<D>(L.cbd[iv[j].v[w]] * mold);  // dequant * mag
+                    const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));                   // lerp_
+                    mu[j][w] = m1;
+                    const uint32_t key = abs_key(m1);
+                    mxk = key > mxk ? key : mxk;
+                }
             }
         }
-        mx = group_max(mx, lpr);
+        const float mx = __uint_as_float(group_max_u32(mxk, lpr));
         const S mag_s = from_f32<S>(mx);
         if (active && lir == 0) mag[rsub] = mag_s;
         const float ms = to_f32(mag_s);
@@ -718,6 +781,16 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
         // with the reciprocal (exact, see div_by_block) and the two-probe search
         const bool fast = two_probe && ms > 0.0f && clamped < __builtin_inff();
         const double rb = fast ? 1.0 / (double)clamped : 0.0;
+        // The bf16 table path rounds the float32 product m1 * r32 instead: m1 and
+        // the magnitude are bf16 values (8-bit significands), so m1 / magnitude is
+        // never a bf16 rounding midpoint and lies at least 2^-17 (relative) away
+        // from every midpoint, while the product is within 2^-23 of it as long as
+        // r32 and the product are normal; then both round to the same bf16 value
+        // as the IEEE quotient.  Rows with magnitudes from 2^100 (r32 near the
+        // subnormal range) and quotients below the table (|x| < 2^-20) take the
+        // float64 quotient.
+        const float r32 = (float)rb;
+        const bool fast32 = fast && clamped < 0x1p100f;
         // output of codeword k before the Nesterov gradient term: q = D(cb_D[k] * mag),
         // then D(q * momentum) with Nesterov
         auto out_base = [&](int k) -> float {
@@ -736,7 +809,10 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
         }
         float sq = 0.0f;  // sum of squares of the outputs this lane writes
         // every row of the wave fast (wave-uniform): the branch-free search below
-        const bool all_fast = __builtin_amdgcn_ballot_w64(!fast) == 0;
+        const bool all_fast = __builtin_amdgcn_ballot_w64(!fast32) == 0;
+        // the element loop, instantiated for T.nesterov (uniform over the workgroup)
+        auto elements = [&](auto nes_tag) {
+        constexpr bool NES = decltype(nes_tag)::value;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             Vec<uint8_t, W> io;
@@ -744,22 +820,26 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
             float sqj = 0.0f;
             int kw[W];
             if (kNb && all_fast) {
-                // the bf16 quotient's bits index nb16 directly; a quotient outside
-                // the table (|x| < 2^-20) takes the two-probe search, once per wave
-                uint32_t miss = 0;
+                // the bf16 quotient's bits index nb16 directly (two quotients per
+                // conversion); the read index is clamped into the table, and a lane
+                // with a quotient outside it (|x| < 2^-20) redoes its vector with
+                // the two-probe search, once per wave
+                bool miss = false;
 #pragma unroll
-                for (int w = 0; w < W; ++w) {
-                    const uint32_t xb = from_f32<bf16_t>(div_by_block(mu[j][w], rb)).bits;
-                    const uint32_t off = (xb & 0x7fffu) - kNb16Lo;
-                    const bool hit = off < kNb16Side;
-                    kw[w] = nb16[hit ? off + ((xb & 0x8000u) ? kNb16Side : 0u) : 0u];
-                    miss |= hit ? 0u : (1u << w);
+                for (int w = 0; w < W; w += 2) {
+                    const uint32_t xb2 = pk_bf16_bits(mu[j][w] * r32, w + 1 < W ? mu[j][w + 1] * r32 : 0.0f);
+#pragma unroll
+                    for (int h = 0; h < 2 && w + h < W; ++h) {
+                        const uint32_t off = ((h ? xb2 >> 16 : xb2) & 0x7fffu) - kNb16Lo;
+                        const int32_t sg = (int32_t)(h ? xb2 : xb2 << 16) >> 31;  // -1 for a negative x
+                        miss |= off >= kNb16Side;
+                        kw[w + h] = nb16[(int32_t)kNb16Side + ((int32_t)min(off, kNb16Side - 1u) ^ sg)];
+                    }
                 }
-                if (__builtin_amdgcn_ballot_w64(miss != 0) != 0) {
+                if (__builtin_amdgcn_ballot_w64(miss) != 0 && miss) {
 #pragma unroll
                     for (int w = 0; w < W; ++w)
-                        if (miss & (1u << w))
-                            kw[w] = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
+                        kw[w] = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
                 }
             } else {
 #pragma unroll
@@ -773,14 +853,42 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
                     }
                 }
             }
+            // the output: a = D(q * momentum) of codeword k (q without Nesterov),
+            // then the Nesterov blend a + g * alpha, one rounding (as muon_blend)
+            if constexpr (kPk) {
 #pragma unroll
-            for (int w = 0; w < W; ++w) {
-                const int k = kw[w];
-                io.v[w] = (uint8_t)k;
-                const float a = TAB ? otab[k] : out_base(k);
-                oo.v[w] = from_f32<D>(muon_blend<D>(a, to_f32(gv[j].v[w]), T));
-                const float o = to_f32(oo.v[w]);
-                sqj = __builtin_fmaf(o, o, sqj);
+                for (int w = 0; w < W; w += 2) {
+                    io.v[w] = (uint8_t)kw[w];
+                    io.v[w + 1] = (uint8_t)kw[w + 1];
+                    float a0, a1;
+                    if (TAB) {
+                        a0 = otab[kw[w]];
+                        a1 = otab[kw[w + 1]];
+                    } else {  // out_base of both codewords, two values per conversion
+                        uint32_t q = pk_bf16_bits(L.cbd[kw[w]] * ms, L.cbd[kw[w + 1]] * ms);
+                        if (NES) q = pk_bf16_bits(__uint_as_float(q << 16) * T.mom, __uint_as_float(q & 0xffff0000u) * T.mom);
+                        a0 = __uint_as_float(q << 16);
+                        a1 = __uint_as_float(q & 0xffff0000u);
+                    }
+                    if (NES) {
+                        a0 = __builtin_fmaf(to_f32(gv[j].v[w]), T.alpha, a0);
+                        a1 = __builtin_fmaf(to_f32(gv[j].v[w + 1]), T.alpha, a1);
+                    }
+                    const uint32_t pk = pk_bf16_bits(a0, a1);
+                    oo.v[w].bits = (uint16_t)pk;
+                    oo.v[w + 1].bits = (uint16_t)(pk >> 16);
+                    sqj = dot2_bf16(pk, sqj);  // + o0^2 + o1^2 (exact products)
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const int k = kw[w];
+                    io.v[w] = (uint8_t)k;
+                    const float a = TAB ? otab[k] : out_base(k);
+                    oo.v[w] = from_f32<D>(muon_blend<D>(a, to_f32(gv[j].v[w]), T));
+                    const float o = to_f32(oo.v[w]);
+                    sqj = __builtin_fmaf(o, o, sqj);
+                }
             }
             const int v = lir + j * lpr;
             if (active && v < T.nvec) {
@@ -790,6 +898,9 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
                 sq += sqj;
             }
         }
+        };
+        if (T.nesterov) elements(std::true_type{});
+        else elements(std::false_type{});
         wsq += sq;
     }
     if (T.sumsq) add_sumsq(wsq, T.sumsq, lw);  // uniform: one task per workgroup

@@ -387,16 +387,48 @@ def test_muon_momentum_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, 
         np.testing.assert_array_equal(np.where(both_nan, 0, got), np.where(both_nan, 0, ref), err_msg="out step {}".format(step))
 
 
+# CodebookTables (gefen_amd/csrc/common.h): cb 256 f32, thr 260 f32, bucket8 4112 u8,
+# bucket 4100 u16, K, max_probe, 2 pad i32, then the 16-byte aligned bf16 table
+_NB16_OFFSET = 14400
+_NB16_LO, _NB16_SIDE = 0x3580, 0x3F82 - 0x3580
+
+
+@pytest.mark.parametrize("cbkind", ["learned", "zero_threshold"])
+def test_bf16_nearest_table_matches_oracle(cbkind):
+    """Every entry of the codebook tables' bf16 nearest-index table (entry
+    side + i for the bf16 bits lo + i, side - 1 - i for their negatives) equals
+    the oracle's nearest search for that value."""
+    print("nb16", cbkind, flush=True)
+    if cbkind == "learned":
+        data, _ = load("exact_dp")
+        cb = np.ascontiguousarray(data["hist_k256_forced/codebook"], dtype=np.float32)
+    else:
+        cb = np.linspace(-1.0, 1.0, 256).astype(np.float32)
+    lib = _lib.load()
+    assert int(lib.gefen_codebook_tables_size()) == _NB16_OFFSET + (2 * _NB16_SIDE + 15) // 16 * 16
+    tables = gu.to_np(_tables(torch.from_numpy(cb).to("cuda:0")))
+    got = tables[_NB16_OFFSET:_NB16_OFFSET + 2 * _NB16_SIDE]
+    i = np.arange(_NB16_SIDE, dtype=np.uint32)
+    bits = np.empty(2 * _NB16_SIDE, np.uint32)
+    bits[_NB16_SIDE + i] = _NB16_LO + i
+    bits[_NB16_SIDE - 1 - i] = 0x8000 | (_NB16_LO + i)
+    x = (bits << 16).view(np.float32)
+    np.testing.assert_array_equal(got, orc.nearest(cb, x).astype(np.uint8))
+
+
 @pytest.mark.parametrize("cbkind", ["learned", "zero_threshold"])
 @pytest.mark.parametrize("block", [2048, 256])
-def test_muon_momentum_quotients_across_forty_octaves(cbkind, block):
+@pytest.mark.parametrize("shifts", [(0,), (-100, 0, 100, 110)])
+def test_muon_momentum_quotients_across_forty_octaves(cbkind, block, shifts):
     """bf16 GefenMuon momentum whose quotients x = m / magnitude spread over
     2^-40 .. 1 (gradients sign * 2^e, e uniform in [-40, 0]): the bf16 nearest
     table covers 2^-20 <= |x| <= 1.0078 and the rest takes the two-probe search.
     With a codebook whose decision threshold between its two middle entries is
     0 (linspace(-1, 1, 256)), +-tiny quotients and zeros land on either side.
-    Bit-exact against the oracle over three steps."""
-    print("muon octaves", cbkind, block, flush=True)
+    Row r's gradients are scaled by 2^shifts[r % len(shifts)]: with (-100, 0,
+    100, 110) rows reach bf16 subnormals and magnitudes beyond 2^100 (which
+    take the float64 quotient).  Bit-exact against the oracle over three steps."""
+    print("muon octaves", cbkind, block, shifts, flush=True)
     if cbkind == "learned":
         data, _ = load("exact_dp")
         cb = np.ascontiguousarray(data["hist_k256_forced/codebook"], dtype=np.float32)
@@ -413,7 +445,8 @@ def test_muon_momentum_quotients_across_forty_octaves(cbkind, block):
     lib = _lib.load()
     for step in range(1, 4):
         e = rng.integers(-40, 1, n).astype(np.float64)
-        g32 = (np.where(rng.random(n) < 0.5, -1.0, 1.0) * np.exp2(e) * (1.0 + rng.random(n))).astype(np.float32)
+        shift = np.asarray(shifts, np.float64)[(np.arange(n) // block) % len(shifts)]
+        g32 = (np.where(rng.random(n) < 0.5, -1.0, 1.0) * np.exp2(e + shift) * (1.0 + rng.random(n))).astype(np.float32)
         g32[rng.random(n) < 0.01] = 0.0
         g = syn.round_to(g32, "bf16").reshape(-1).copy()
         g_dev = gu.to_dev(g, "bf16")
