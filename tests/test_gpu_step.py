@@ -417,7 +417,7 @@ def test_bf16_nearest_table_matches_oracle(cbkind):
 
 
 @pytest.mark.parametrize("cbkind", ["learned", "zero_threshold"])
-@pytest.mark.parametrize("block", [2048, 256])
+@pytest.mark.parametrize("block", [2048, 1536, 256])
 @pytest.mark.parametrize("shifts", [(0,), (-100, 0, 100, 110)])
 def test_muon_momentum_quotients_across_forty_octaves(cbkind, block, shifts):
     """bf16 GefenMuon momentum whose quotients x = m / magnitude spread over
