@@ -21,11 +21,16 @@ written into the same gradient buffers (outside the timed region).
   frac_of_copy the step kernels' bandwidth as a fraction of it.
 * cpu_baseline: the CPU oracle (C restatement of the reference CPU path,
   OpenMP) on a bounded sample of the same tensors, scaled to a full step.
+* other_configs (default config only, unless --headline-only): the metric's
+  other named shapes, GPT-2 124M (fp32) and Llama-3 1.5B (bf16), and the
+  GefenMuon Qwen3-1.7B step, each measured the same way in the same run after
+  the 8B tensors are freed (step ms, kernel roofline; no CPU baseline).
 """
 
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -506,37 +511,15 @@ def cpu_baseline_kernels(g_host, period_divs):
                       "thread)".format((t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3)}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS) + ["kernels"])
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also copy 2 GiB once with k_copy16 (a kernel of known traffic for scaling HBM counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
-              "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
-        sys.exit(2)
-    dev = torch.device("cuda:0")
-    if args.config == "kernels":
-        bench_kernels(args, dev)
-        return
-    cfg = CONFIGS[args.config]
+def measure(name, args, dev, with_cpu, copy_gbs=None):
+    """One config's JSON object: median step() latency over args.steps timed steps
+    after args.warmup untimed ones (new gradients before every step), the
+    kernel roofline, and (with_cpu) the CPU baseline."""
+    cfg = CONFIGS[name]
     from gefen_amd.gefen import Gefen
     from gefen_amd.gefen_muon import GefenMuon
     from gefen_amd import _lib
 
-    if args.copy_probe:
-        from gefen_amd import synthetic as syn
-
-        src = torch.ones(1 << 30, dtype=torch.int16, device=dev)
-        dst = torch.empty_like(src)
-        syn.copy_device(src, dst)  # k_copy16: 2 GiB read + 2 GiB written
-        torch.cuda.synchronize()
-        del src, dst
     params = build_problem(cfg, dev)
 
     def set_grads(k):
@@ -576,8 +559,8 @@ def main():
            "config": {"workload": cfg["workload"], "tensors": len(params),
                       "params": int(sum(p.numel() for _, p in params))},
            "p10_ms": round(q[0], 4), "p90_ms": round(q[1], 4), "first_step_ms": round(first_ms, 1)}
-    if args.config in PUBLISHED_MS:
-        out["vs_baseline"] = round(PUBLISHED_MS[args.config] / med, 3)
+    if name in PUBLISHED_MS:
+        out["vs_baseline"] = round(PUBLISHED_MS[name] / med, 3)
     periods = {}
     for _, p in params:
         P = opt.state[p]["automatic_period"]
@@ -601,17 +584,73 @@ def main():
         kms = e0.elapsed_time(e1) / reps
         nbytes = step_bytes(opt, params)
         achieved = nbytes / (kms * 1e-3) / 1e9
-        copy_gbs = copy_ceiling_gbs(dev)
+        if copy_gbs is None:
+            copy_gbs = copy_ceiling_gbs(dev)
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg, nbytes),
                            "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes),
                            "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
-        if not args.no_cpu_baseline:
+        if with_cpu:
             out["cpu_baseline"] = cpu_baseline(opt, params)
     else:
         out["roofline"] = muon_ns_roofline(opt, params)
-        if not args.no_cpu_baseline:
+        if with_cpu:
             out["cpu_baseline"] = cpu_baseline_muon(opt, params)
+    return out
+
+
+def compact(out):
+    """The figures of a further config's line that the headline line carries."""
+    r = out["roofline"]
+    keep = ("bound", "achieved", "peak", "unit", "frac", "kernel_ms_per_step", "frac_of_copy")
+    return {"workload": out["config"]["workload"], "ms_per_step": out["value"], "p10_ms": out["p10_ms"],
+            "p90_ms": out["p90_ms"], "first_step_ms": out["first_step_ms"], "dtype": out["dtype"],
+            "vs_readme": out["vs_baseline"], "periods": out["config"]["periods"],
+            "roofline": {k: r[k] for k in keep if k in r}}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="llama8b", choices=sorted(CONFIGS) + ["kernels"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="with the default config, skip the GPT-2, Llama-1.5B and GefenMuon lines that the "
+                         "headline line otherwise carries under other_configs")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also copy 2 GiB once with k_copy16 (a kernel of known traffic for scaling HBM counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
+              "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    if args.config == "kernels":
+        bench_kernels(args, dev)
+        return
+    if args.copy_probe:
+        from gefen_amd import synthetic as syn
+
+        src = torch.ones(1 << 30, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        syn.copy_device(src, dst)  # k_copy16: 2 GiB read + 2 GiB written
+        torch.cuda.synchronize()
+        del src, dst
+    out = measure(args.config, args, dev, not args.no_cpu_baseline)
+    if args.config == "llama8b" and not args.headline_only:
+        # the metric's other named shapes (and GefenMuon), each measured the same
+        # way after the headline's tensors are freed; value stays the 8B step
+        others = {}
+        for name in ("gpt2", "llama1.5b", "muon"):
+            gc.collect()
+            torch.cuda.empty_cache()
+            try:
+                others[name] = compact(measure(name, args, dev, False, out["roofline"].get("copy_kernel_gbs")))
+            except Exception as e:  # the headline line is printed regardless
+                others[name] = {"error": repr(e)[:300]}
+        out["other_configs"] = others
     print(json.dumps(out), flush=True)
 
 

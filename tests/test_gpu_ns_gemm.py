@@ -73,6 +73,9 @@ def _nt_batched(a, b, out, out_t=None, d=None, alpha=1.0, beta=0.0, symmetric=Fa
     (4, 512, 512, 768, 1.0, 0.0, True, False),
     (2, 768, 768, 768, 2.0315, -4.775, True, False),
     (2, 512, 512, 512, 2.0315, -4.775, True, True),
+    (2, 768, 512, 128, 1.0, 0.75, False, True),          # two K steps, M > N, D given as D^T
+    (2, 512, 768, 192, 1.0, -2.0, False, True),          # odd K step count
+    (2, 512, 512, 1024, 2.0315, -4.775, True, True),
 ])
 def test_batched_gemm_equals_one_matrix_gemm(g, m, n, k, alpha, beta, sym, dt):
     """The batched large-tile GEMM accumulates K in the same MFMA order as the
