@@ -152,6 +152,54 @@ def test_gpt2_124m_fp32_full_config_matches_oracle():
     _run("gpt2")
 
 
+def test_gpt2_124m_fp32_twenty_free_running_steps_match_oracle():
+    """The GPT-2 124M fp32 configuration over 20 steps (a new gradient each step)
+    with the oracle running on its own for the sampled tensors, never resynchronised
+    from the GPU: the momentum state depends only on the gradients, so codebook
+    indices and magnitudes stay bit-exact at every step, and the parameters meet
+    the north star's bound after 20 steps (rtol 1e-5, atol 1e-7; the float32
+    block mean of g^2 is summed in another order, within rtol 2^-18 per step)."""
+    import bench
+    from gefen_amd.gefen import Gefen
+
+    cfg = bench.CONFIGS["gpt2"]
+    dev = torch.device("cuda:0")
+    params = bench.build_problem(cfg, dev)
+    opt = Gefen(params)
+    opt.step()
+    torch.cuda.synchronize()
+    sample = _sample(params, opt)
+    grads = [_host(p.grad) for _, p in params]
+    ref_cb = orc.learn_codebook([(g, "f32", opt.state[p]["automatic_period"]) for g, (_, p) in zip(grads, params)])
+    np.testing.assert_array_equal(opt._gefen_codebook.detach().cpu().numpy(), ref_cb)
+    arrs = [{"p": _initial(cfg, params, i), "dtype": "f32", "shape": tuple(params[i][1].shape), "lr": 1e-3,
+             "beta1": 0.9, "beta2": 0.999, "eps": 1e-8, "weight_decay": 0.0} for i in sample]
+    ref = orc.GefenOracle(arrs, codebook=ref_cb)
+    ref.step([grads[i] for i in sample])  # the oracle predicts its own periods
+    del grads
+    assert ref.periods == [opt.state[params[i][1]]["automatic_period"] for i in sample]
+    for step in range(2, 21):
+        for i, (_, p) in enumerate(params):
+            bench.fill_grad(cfg, p.grad, i, step)
+        opt.step()
+        torch.cuda.synchronize()
+        ref.step([_host(params[i][1].grad) for i in sample])
+        for k, i in enumerate(sample):
+            st = opt.state[params[i][1]]
+            tag = "gpt2 {} step {}".format(params[i][0], step)
+            np.testing.assert_array_equal(_host(st["m_codebook"]), ref.state[k].m_codebook, err_msg=tag)
+            np.testing.assert_array_equal(_host(st["m_magnitude"]), ref.state[k].m_magnitude, err_msg=tag)
+    for k, i in enumerate(sample):
+        name, p = params[i]
+        np.testing.assert_allclose(_host(p), ref.params[k]["p"], rtol=1e-5, atol=1e-7, err_msg=name + " params")
+        np.testing.assert_allclose(_host(opt.state[p]["vmean"]), ref.state[k].vmean, rtol=2.0 ** -16, atol=0,
+                                   err_msg=name + " vmean")
+        err = np.abs(_host(p).astype(np.float64) - ref.params[k]["p"])
+        print("gpt2", name, "period", ref.periods[k], "20 steps: indices and magnitudes exact; params max |diff|",
+              float(err.max()), "= {:.3f} of the tolerance".format(
+                  float(np.max(err / (1e-7 + 1e-5 * np.abs(ref.params[k]["p"]))))), flush=True)
+
+
 def test_llama_1_5b_bf16_full_config_matches_oracle():
     _run("llama1.5b")
 
