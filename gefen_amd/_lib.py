@@ -61,6 +61,8 @@ SIGNATURES = {
     "gefen_gemm_bf16_nt_batched": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, I32,
                                          I32, I32, I32, DBL, DBL, I32, P]),
     "gefen_gram_bf16_batched": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, DBL, P]),
+    "gefen_gemm_bf16_nt_batched_apply": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, I32, I32, I32, I32, DBL, DBL,
+                                               P, P]),
 }
 
 # numpy mirror of struct gefen_step_task / gefen_muon_task (natural C alignment)

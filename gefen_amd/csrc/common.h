@@ -61,6 +61,21 @@ __device__ __forceinline__ T from_f32(float v) { return Conv<T>::from(v); }
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
 
+// GefenMuon's update of one parameter element in dtype D (gefen_muon.py:325-329):
+// p.mul_(1 - lr * wd), rounded to D, when decaying; then p.add_(u, alpha) as
+// torch evaluates it: one fma for float32; for a reduced dtype (alpha already
+// rounded to D) the product u * alpha is exact in float32, rounded to D first
+// when the update is a transposed view (torch's element-wise path), and added.
+template <typename D>
+__device__ __forceinline__ float muon_apply_value(float pf, float uf, float wdf, float alpha, bool do_wd,
+                                                  bool round_prod) {
+    if (do_wd) pf = round_to<D>(pf * wdf);
+    if constexpr (sizeof(D) == 4) return __builtin_fmaf(uf, alpha, pf);
+    float prod = uf * alpha;
+    if (round_prod) prod = round_to<D>(prod);
+    return pf + prod;
+}
+
 // NaN-propagating maximum of non-negative values (torch amax semantics)
 __device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
 // Maximum that skips NaN: b replaces a only when b > a, a comparison NaN never

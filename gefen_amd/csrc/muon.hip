@@ -224,11 +224,7 @@ struct ApplyBatch {
 
 template <typename D>
 __device__ __forceinline__ float apply_one(float pf, float uf, const ApplyTask& T) {
-    if (T.do_wd) pf = round_to<D>(pf * T.wdf);  // p.mul_(1 - lr * wd)
-    if constexpr (sizeof(D) == 4) return __builtin_fmaf(uf, T.alpha, pf);  // p.add_(u, alpha): one fma
-    float prod = uf * T.alpha;                                              // exact: bf16 * reduced alpha
-    if (T.round_prod) prod = round_to<D>(prod);
-    return pf + prod;
+    return muon_apply_value<D>(pf, uf, T.wdf, T.alpha, T.do_wd, T.round_prod);
 }
 
 template <typename D>
@@ -374,23 +370,11 @@ extern "C" int gefen_muon_apply_tasks(const gefen_muon_apply_task* tasks, int nt
             t.p = in.p;
             t.u = static_cast<const uint16_t*>(in.update);
             t.numel = in.numel;
-            t.wdf = (float)(1.0 - in.lr * in.weight_decay);
-            t.do_wd = in.weight_decay > 0.0;
-            const float a32 = (float)(-in.adjusted_lr);
-            if (dt == GEFEN_F32) {
-                t.alpha = a32;
-            } else {  // torch.tensor(-lr_adj, float32).to(dtype).float()
-                uint32_t u;
-                memcpy(&u, &a32, 4);
-                if (dt == GEFEN_BF16) {
-                    u += 0x7fffu + ((u >> 16) & 1u);
-                    u &= 0xffff0000u;
-                    memcpy(&t.alpha, &u, 4);
-                } else {
-                    t.alpha = (float)(_Float16)a32;
-                }
-            }
-            t.round_prod = (dt != GEFEN_F32 && in.transposed) ? 1 : 0;
+            const MuonApplyScalars sc = muon_apply_scalars(in);
+            t.wdf = sc.wdf;
+            t.alpha = sc.alpha;
+            t.do_wd = sc.do_wd;
+            t.round_prod = sc.round_prod;
             const int esz = dtype_size(dt);
             t.vec = aligned(in.p, 8 * esz) && aligned(in.update, 16) ? 1 : 0;
             t.nwg = (int32_t)nwg;

@@ -17,6 +17,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "capi_internal.h"
 #include "common.h"
 
@@ -331,9 +333,25 @@ constexpr int LDT = TM + 4;
 static_assert(TM == TN, "square tiles");
 static_assert(TN * LDT <= 4 * TM * TLD, "the epilogue tile fits in the operand stages");
 
+// GefenMuon's parameter update fused into the last Newton-Schulz product
+// (gefen_gemm_bf16_nt_batched_apply): matrix b of a launch is the update U of
+// parameter p[b], whose layout is U (rows of N elements) or, when transposed, U^T
+// (rows of M elements); the other entries are the scalars of muon_apply_value.
+constexpr int kMaxFuse = 64;  // matrices per launch (the table travels in the kernel arguments)
+struct FusedApply {
+    void* p[kMaxFuse];
+    float wdf[kMaxFuse];
+    float alpha[kMaxFuse];
+    uint8_t do_wd[kMaxFuse];
+    uint8_t round_prod[kMaxFuse];
+    int32_t transposed;
+};
+
 // MN: both operands MN-major (the symmetric Gram product from X^T; no D, no C^T).
-template <bool MN>
-__global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
+// PD: void, or the parameter type of a fused update (fa != nullptr; C and C^T
+// are then not stored).
+template <bool MN, typename PD>
+__device__ __forceinline__ void gemm_tile_body(const TileGemm& g, const FusedApply* fa) {
     // operand stages: A in [0, 2) and B in [2, 4) of TM x TLD each; the epilogue reuses them
     __shared__ __attribute__((aligned(16))) uint16_t smem[4 * TM * TLD];
     uint16_t* const As[2] = {smem, smem + TM * TLD};
@@ -533,6 +551,47 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
             }
         }
     __syncthreads();
+    if constexpr (!std::is_void<PD>::value) {
+        // T holds the update tile as U^T (bf16): p <- muon_apply_value(p, U) with
+        // 8-element chunks of parameter rows, read and written once
+        PD* __restrict__ P = static_cast<PD*>(fa->p[batch]);
+        const float wdf = fa->wdf[batch], al = fa->alpha[batch];
+        const bool dwd = fa->do_wd[batch] != 0, rp = fa->round_prod[batch] != 0;
+        auto update8 = [&](int64_t e, const uint32_t (&w)[4]) {
+            Vec<PD, 8> pv = vload<PD, 8>(P, e);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float uf = __uint_as_float((u & 1) ? (w[u >> 1] & 0xffff0000u) : (w[u >> 1] << 16));
+                pv.v[u] = from_f32<PD>(muon_apply_value<PD>(to_f32(pv.v[u]), uf, wdf, al, dwd, rp));
+            }
+            vstore<PD, 8>(P, e, pv);
+        };
+        if (fa->transposed) {  // parameter rows are rows of U^T: T row c -> row n0 + c
+#pragma unroll
+            for (int i = 0; i < kChunks; ++i) {
+                const int q = threadIdx.x + TT * i;
+                const int c = q >> 5, r8 = (q & 31) * 8;
+                const uint2* t = reinterpret_cast<const uint2*>(T + c * LDT + r8);
+                const uint2 lo = t[0], hi = t[1];
+                const uint32_t w[4] = {lo.x, lo.y, hi.x, hi.y};
+                update8((int64_t)(n0 + c) * g.M + m0 + r8, w);
+            }
+        } else {  // parameter rows are rows of U, gathered from two column chunks as C below
+#pragma unroll
+            for (int i = 0; i < kChunks; ++i) {
+                const int q = threadIdx.x + TT * i;
+                const int r = (q & 31) + 32 * (q >> 10), c8 = ((q >> 5) & 31) * 8;
+                const uint16_t* t = T + c8 * LDT + r;
+                uint32_t h[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) h[u] = t[u * LDT];
+                const uint32_t w[4] = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                       h[6] | (h[7] << 16)};
+                update8((int64_t)(m0 + r) * g.N + n0 + c8, w);
+            }
+        }
+        return;
+    }
     if (CT || mirror) {  // rows of C^T: T row c -> row n0 + c
         uint16_t* __restrict__ dst = CT ? CT : C;
         const int64_t ld = CT ? g.ldct : g.ldc;
@@ -565,6 +624,16 @@ __global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
         v.w = h[6] | (h[7] << 16);
         *reinterpret_cast<u32x4*>(C + (int64_t)(m0 + r) * g.ldc + n0 + c8) = v;
     }
+}
+
+template <bool MN>
+__global__ __launch_bounds__(TT) void k_gemm_tile(const TileGemm g) {
+    gemm_tile_body<MN, void>(g, nullptr);
+}
+
+template <typename PD>
+__global__ __launch_bounds__(TT) void k_gemm_tile_apply(const TileGemm g, const FusedApply fa) {
+    gemm_tile_body<false, PD>(g, &fa);
 }
 
 }  // namespace ns
@@ -679,4 +748,81 @@ extern "C" int gefen_gram_bf16_batched(const void* xt, int64_t ldxt, int64_t str
     hipLaunchKernelGGL(ns::k_gemm_tile<true>, dim3((unsigned)grid), dim3(ns::TT), 0, reinterpret_cast<hipStream_t>(stream),
                        g);
     return launch_status("gefen_gram_bf16_batched");
+}
+
+extern "C" int gefen_gemm_bf16_nt_batched_apply(const void* a, int64_t lda, int64_t stride_a, const void* b,
+                                                int64_t ldb, int64_t stride_b, const void* d_t, int64_t ldd,
+                                                int64_t stride_d, int batch, int m, int n, int k, double alpha,
+                                                double beta, const gefen_muon_apply_task* tasks,
+                                                gefen_stream_t stream) {
+    if (m < 0 || n < 0 || k < 0 || batch < 0) return fail_inval("negative GEMM size");
+    if (m == 0 || n == 0 || batch == 0) return GEFEN_OK;
+    if (!a || !b || !tasks || (beta != 0.0 && !d_t)) return fail_inval("null GEMM operand");
+    if (lda < k || ldb < k || (beta != 0.0 && ldd < m)) return fail_inval("GEMM leading dimension too small");
+    if ((int64_t)ns::TM * lda * 2 > INT32_MAX || (int64_t)ns::TN * ldb * 2 > INT32_MAX)
+        return fail_inval("batched GEMM operand rows too long (256 rows must span less than 2^31 bytes)");
+    if (m % ns::TM || n % ns::TN || k % ns::TK || k == 0)
+        return fail_inval("batched GEMM needs M, N multiples of 256 and K a multiple of %d (got %d, %d, %d)", ns::TK, m, n, k);
+    const void* ptrs[3] = {a, b, beta != 0.0 ? d_t : nullptr};
+    const int64_t lds_[3] = {lda, ldb, ldd};
+    const int64_t strides[3] = {stride_a, stride_b, stride_d};
+    for (int i = 0; i < 3; ++i) {
+        if (!ptrs[i]) continue;
+        if (!aligned(ptrs[i], 16) || lds_[i] % 8 || strides[i] % 8)
+            return fail_inval("batched GEMM operands need 16-byte aligned rows");
+    }
+    const int dt = tasks[0].param_dtype;
+    const int transposed = tasks[0].transposed ? 1 : 0;
+    if (!valid_dtype(dt)) return fail_inval("unsupported parameter dtype %d", dt);
+    for (int i = 0; i < batch; ++i) {
+        const gefen_muon_apply_task& t = tasks[i];
+        if (t.param_dtype != dt) return fail_inval("the parameters of one call must share a dtype");
+        if ((t.transposed ? 1 : 0) != transposed) return fail_inval("the parameters of one call must share an orientation");
+        if (t.numel != (int64_t)m * n) return fail_inval("parameter %d has %lld elements, the product %lld", i,
+                                                        (long long)t.numel, (long long)m * n);
+        if (!t.p) return fail_inval("null parameter pointer");
+        if (!aligned(t.p, 8 * dtype_size(dt))) return fail_inval("parameters need %d-byte alignment", 8 * dtype_size(dt));
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int tiles = (m / ns::TM) * (n / ns::TN);
+    for (int c0 = 0; c0 < batch; c0 += ns::kMaxFuse) {
+        const int nb = batch - c0 < ns::kMaxFuse ? batch - c0 : ns::kMaxFuse;
+        ns::TileGemm g;
+        memset(&g, 0, sizeof(g));
+        g.A = static_cast<const uint16_t*>(a) + c0 * stride_a;
+        g.B = static_cast<const uint16_t*>(b) + c0 * stride_b;
+        g.D = beta != 0.0 ? static_cast<const uint16_t*>(d_t) + c0 * stride_d : nullptr;
+        g.lda = lda; g.ldb = ldb; g.ldd = ldd;
+        g.sa = stride_a; g.sb = stride_b; g.sd = stride_d;
+        g.M = m; g.N = n; g.K = k;
+        g.alpha = (float)alpha;
+        g.beta = (float)beta;
+        g.tiles_n = n / ns::TN;
+        g.symmetric = 0;
+        g.tiles = tiles;
+        g.d_t = 1;
+        if (g.D && ldd % 4) return fail_inval("D^T rows must be 8-byte aligned");
+        ns::FusedApply fa;
+        memset(&fa, 0, sizeof(fa));
+        fa.transposed = transposed;
+        for (int i = 0; i < nb; ++i) {
+            const MuonApplyScalars sc = muon_apply_scalars(tasks[c0 + i]);
+            fa.p[i] = tasks[c0 + i].p;
+            fa.wdf[i] = sc.wdf;
+            fa.alpha[i] = sc.alpha;
+            fa.do_wd[i] = (uint8_t)sc.do_wd;
+            fa.round_prod[i] = (uint8_t)sc.round_prod;
+        }
+        const int64_t grid = (int64_t)tiles * nb;
+        if (grid > INT32_MAX) return fail_inval("batched GEMM grid too large");
+        if (dt == GEFEN_F32)
+            hipLaunchKernelGGL(ns::k_gemm_tile_apply<float>, dim3((unsigned)grid), dim3(ns::TT), 0, st, g, fa);
+        else if (dt == GEFEN_BF16)
+            hipLaunchKernelGGL(ns::k_gemm_tile_apply<bf16_t>, dim3((unsigned)grid), dim3(ns::TT), 0, st, g, fa);
+        else
+            hipLaunchKernelGGL(ns::k_gemm_tile_apply<f16_t>, dim3((unsigned)grid), dim3(ns::TT), 0, st, g, fa);
+        const int rc = launch_status("gefen_gemm_bf16_nt_batched_apply");
+        if (rc) return rc;
+    }
+    return GEFEN_OK;
 }

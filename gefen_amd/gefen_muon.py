@@ -305,7 +305,11 @@ class _MuonPlan:
     layout, the state tensors are the same objects and each group's Newton-Schulz
     settings (coefficients, steps, eps, lr adjustment) are unchanged; it then
     refreshes gradient addresses, step counts, lr, weight decay, momentum and
-    Nesterov, and returns True.  Otherwise it changes nothing and returns False."""
+    Nesterov, and returns True.  Otherwise it changes nothing and returns False.
+    A stack with Newton-Schulz steps applies its parameters' updates inside its
+    last product (gefen_gemm_bf16_nt_batched_apply), so the updates are never
+    stored and read back; the first step (the table build) applies them with
+    gefen_muon_apply_tasks, which the plan's results equal bit for bit."""
 
     def __init__(self, opt, items, mtasks, apply, stacks, device, sumsq):
         self.params = [it[1] for it in items]
@@ -326,6 +330,13 @@ class _MuonPlan:
         self.mtasks = mtasks.copy()
         self.apply = apply.copy()
         self.stacks = stacks
+        # stacks with Newton-Schulz steps apply their updates in their last product
+        # (gefen_gemm_bf16_nt_batched_apply); the other tensors take gefen_muon_apply_tasks
+        fused = np.zeros(len(items), dtype=bool)
+        for key, idx, _, _, _ in stacks:
+            if key[4] > 0:
+                fused[idx] = True
+        self.rest = np.nonzero(~fused)[0]
         self.sumsq = sumsq
         self.settings = self._settings()
         self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.state_keys)
@@ -386,11 +397,17 @@ class _MuonPlan:
             for key, idx, buf, work, sum_index in self.stacks:
                 coeffs, steps, eps = key[3], key[4], key[5]
                 x = buf if key[2] == torch.bfloat16 else buf.bfloat16()
-                res = newton_schulz_batched(x, coeffs, steps, eps, work=work,
-                                            sumsq=self.sumsq if sum_index is not None else None, index=sum_index)
+                sums = self.sumsq if sum_index is not None else None
+                if steps > 0:  # the last product updates the parameters (gefen_muon.py:47, 325-329)
+                    newton_schulz_batched(x, coeffs, steps, eps, work=work, sumsq=sums, index=sum_index,
+                                          apply=self.apply[idx])
+                    keep.append(x)
+                    continue
+                res = newton_schulz_batched(x, coeffs, steps, eps, work=work, sumsq=sums, index=sum_index)
                 keep.append((x, res))
                 slot_bytes = res[0].numel() * res.element_size()
                 self.apply["update"][idx] = res.data_ptr() + np.arange(len(idx), dtype=np.uint64) * slot_bytes
-            _lib.check(lib.gefen_muon_apply_tasks(self.apply.ctypes.data, len(self.apply), stream),
-                       "gefen_muon_apply_tasks")
+            if len(self.rest):
+                rest = np.ascontiguousarray(self.apply[self.rest])
+                _lib.check(lib.gefen_muon_apply_tasks(rest.ctypes.data, len(rest), stream), "gefen_muon_apply_tasks")
             del keep

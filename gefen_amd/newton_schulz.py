@@ -16,6 +16,7 @@ from __future__ import annotations
 
 from typing import Optional, Tuple
 
+import numpy as np
 import torch
 
 from gefen_amd import _lib
@@ -95,6 +96,27 @@ def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: 
     _lib.check(rc, "gefen_gemm_bf16_nt_batched")
 
 
+def gemm_nt_batched_apply(a: torch.Tensor, b: torch.Tensor, d_t: Optional[torch.Tensor], alpha: float, beta: float,
+                          tasks) -> None:
+    """U[i] = alpha * a[i] @ b[i]^T + beta * D[i] (D given as its transpose d_t),
+    applied as GefenMuon's update of parameter tasks[i] (a MUON_APPLY_TASK array,
+    one row per matrix; U[i] is the parameter's layout, or its transpose when
+    tasks[i].transposed) instead of being stored."""
+    g, m, k = a.shape
+    n = b.shape[1]
+    if len(tasks) != g:
+        raise ValueError("one apply task per matrix")
+    tasks = np.ascontiguousarray(tasks)
+    lib = _lib.load()
+    rc = lib.gefen_gemm_bf16_nt_batched_apply(a.data_ptr(), a.stride(1), a.stride(0), b.data_ptr(), b.stride(1),
+                                              b.stride(0), d_t.data_ptr() if d_t is not None else None,
+                                              d_t.stride(1) if d_t is not None else 0,
+                                              d_t.stride(0) if d_t is not None else 0, g, m, n, k, float(alpha),
+                                              float(beta), tasks.ctypes.data,
+                                              torch.cuda.current_stream(a.device).cuda_stream)
+    _lib.check(rc, "gefen_gemm_bf16_nt_batched_apply")
+
+
 def gram_batched(xt: torch.Tensor, out: torch.Tensor) -> None:
     """out[i] = X[i] @ X[i]^T for the stacked X[i]^T = xt[i] ([k, m] bf16, row-major)."""
     g, k, m = xt.shape
@@ -106,7 +128,7 @@ def gram_batched(xt: torch.Tensor, out: torch.Tensor) -> None:
 
 def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], steps: int,
                           eps: float, work: Optional[dict] = None, sumsq: Optional[torch.Tensor] = None,
-                          index: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          index: Optional[torch.Tensor] = None, apply=None) -> Optional[torch.Tensor]:
     """Newton-Schulz of every matrix of a [G, rows, cols] bf16 stack; returns the
     [G, rows, cols] result.  x's values may be overwritten.
 
@@ -115,8 +137,13 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
     call with the same number of steps.
     sumsq, index: the matrices' sums of squares, already gathered (float64 device
     tensor; matrix g's is sumsq[index[g]], int32 device index, or sumsq[g]), so
-    the normalisation does not read the stack twice."""
+    the normalisation does not read the stack twice.
+    apply: GefenMuon's update tasks of the stack's parameters (a MUON_APPLY_TASK
+    array, one row per matrix, steps > 0): the last product is applied to them
+    (gemm_nt_batched_apply) instead of returned, and the result is None."""
     a, b, c = coeffs
+    if apply is not None and steps <= 0:
+        raise ValueError("a fused update needs at least one Newton-Schulz step")
     g, rows, cols = x.shape
     transposed = rows > cols
     m, n = (cols, rows) if transposed else (rows, cols)  # X [m, n], m <= n
@@ -158,6 +185,9 @@ def newton_schulz_batched(x: torch.Tensor, coeffs: Tuple[float, float, float], s
         for it in range(steps):
             gram_batched(xt, gram)                                                        # X X^T
             gemm_nt_batched(gram, gram, upd, d_t=gram, alpha=c, beta=b, symmetric=True)   # b A + c A A
+            if it + 1 == steps and apply is not None:
+                gemm_nt_batched_apply(upd, xt, xt, 1.0, a, apply)                        # p += adj * (a X + B X)
+                return None
             if it + 1 < steps or transposed:
                 gemm_nt_batched(upd, xt, None, out_t=nxt, d_t=xt, alpha=1.0, beta=a)      # (a X + B X)^T
                 xt, nxt = nxt, xt

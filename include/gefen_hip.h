@@ -219,6 +219,21 @@ typedef struct gefen_muon_apply_task {
 
 int gefen_muon_apply_tasks(const gefen_muon_apply_task* tasks, int ntasks, gefen_stream_t stream);
 
+/* The last Newton-Schulz product of a stack applied as GefenMuon's parameter
+ * update instead of being stored (no single reference counterpart: it is
+ * gefen_muon.py:47 followed by gefen_muon.py:325-329 in one pass, so the update
+ * is never written to memory and read back).  For each matrix i of the stack,
+ *   U_i = bf16(alpha * A_i @ B_i^T + beta * D_i)
+ * as gefen_gemm_bf16_nt_batched forms it (D given as its transpose d_t [n, m]),
+ * and parameter tasks[i].p (numel m * n; layout U_i, or U_i^T when
+ * tasks[i].transposed) is updated exactly as gefen_muon_apply_tasks updates it
+ * with update = U_i (tasks[i].update is not read).  All tasks share one
+ * parameter dtype and orientation; parameters are 8-element aligned. */
+int gefen_gemm_bf16_nt_batched_apply(const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
+                                     int64_t stride_b, const void* d_t, int64_t ldd, int64_t stride_d, int batch,
+                                     int m, int n, int k, double alpha, double beta,
+                                     const gefen_muon_apply_task* tasks, gefen_stream_t stream);
+
 /* ------------------------------------------------------------------ first step
  * Replaces gefen_exact_histogram_cuda (exact_histogram_fused.py:10-58,
  * exact_histogram_fused_kernel.cu:131-160): per block absmax normalisation,

@@ -1,6 +1,8 @@
 """MFMA bf16 GEMM of the Newton-Schulz iteration against an fp32 PyTorch reference
 of the same op (products in fp32 on the CPU, one bf16 rounding)."""
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -237,3 +239,56 @@ def test_batched_newton_schulz_keeps_only_the_transpose_bit_exactly(g, rows, col
     torch.cuda.synchronize()
     assert got.shape == ref.shape == x0.shape
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype,transposed,wd,batch", [
+    (torch.bfloat16, False, 0.1, 3),
+    (torch.bfloat16, True, 0.0, 3),
+    (torch.float32, False, 0.0, 2),
+    (torch.float32, True, 0.1, 2),
+    (torch.float16, True, 0.1, 2),
+    (torch.bfloat16, True, 0.1, 70),   # two launches of at most 64 matrices
+])
+def test_fused_update_equals_product_then_apply(dtype, transposed, wd, batch):
+    """gefen_gemm_bf16_nt_batched_apply (the last Newton-Schulz product applied as
+    GefenMuon's update) equals storing the product with gefen_gemm_bf16_nt_batched
+    and applying it with gefen_muon_apply_tasks, bit for bit, for every parameter
+    dtype, both orientations and with / without weight decay."""
+    import numpy as np
+    from gefen_amd import _lib
+    from gefen_amd.newton_schulz import gemm_nt_batched_apply
+
+    m, n, k = (256, 512, 256) if batch <= 3 else (256, 256, 256)
+    gen = torch.Generator(device="cpu").manual_seed(batch * 10 + int(transposed) + (wd > 0) * 100)
+    a = (torch.randn(batch, m, k, generator=gen) * 0.05).bfloat16().cuda()
+    b = (torch.randn(batch, n, k, generator=gen) * 0.05).bfloat16().cuda()
+    d_t = (torch.randn(batch, n, m, generator=gen) * 0.05).bfloat16().cuda()
+    shape = (n, m) if transposed else (m, n)
+    p0 = (torch.randn(batch, *shape, generator=gen) * 0.02).to(dtype).cuda()
+    p_fused, p_ref = p0.clone(), p0.clone()
+
+    def tasks(params, update):
+        t = np.zeros(batch, dtype=_lib.MUON_APPLY_TASK)
+        for i in range(batch):
+            t[i]["p"] = params[i].data_ptr()
+            t[i]["update"] = update[i].data_ptr() if update is not None else 0
+            t[i]["numel"] = params[i].numel()
+            t[i]["param_dtype"] = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+            t[i]["transposed"] = 1 if transposed else 0
+            t[i]["lr"] = 0.02
+            t[i]["weight_decay"] = wd
+            t[i]["adjusted_lr"] = 0.02 * 0.2 * math.sqrt(max(m, n))
+        return t
+
+    gemm_nt_batched_apply(a, b, d_t, 1.0, 3.4445, tasks(p_fused, None))
+    if transposed:
+        u = torch.empty(batch, n, m, dtype=torch.bfloat16, device="cuda:0")
+        _nt_batched(a, b, None, out_t=u, d_t=d_t, alpha=1.0, beta=3.4445)
+    else:
+        u = torch.empty(batch, m, n, dtype=torch.bfloat16, device="cuda:0")
+        _nt_batched(a, b, u, d_t=d_t, alpha=1.0, beta=3.4445)
+    t = tasks(p_ref, u)
+    _lib.check(_lib.load().gefen_muon_apply_tasks(t.ctypes.data, batch, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert not torch.equal(p_fused, p0)
+    assert torch.equal(p_fused.view(torch.uint8), p_ref.view(torch.uint8))
