@@ -553,42 +553,45 @@ __device__ __forceinline__ void gemm_tile_body(const TileGemm& g, const FusedApp
     __syncthreads();
     if constexpr (!std::is_void<PD>::value) {
         // T holds the update tile as U^T (bf16): p <- muon_apply_value(p, U) with
-        // 8-element chunks of parameter rows, read and written once
+        // 8-element chunks of parameter rows, read and written once; every chunk's
+        // load is issued before the first update (the accumulators are dead here)
         PD* __restrict__ P = static_cast<PD*>(fa->p[batch]);
         const float wdf = fa->wdf[batch], al = fa->alpha[batch];
         const bool dwd = fa->do_wd[batch] != 0, rp = fa->round_prod[batch] != 0;
-        auto update8 = [&](int64_t e, const uint32_t (&w)[4]) {
-            Vec<PD, 8> pv = vload<PD, 8>(P, e);
+        const bool tr = fa->transposed != 0;
+        int64_t e[kChunks];
+        Vec<PD, 8> pv[kChunks];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float uf = __uint_as_float((u & 1) ? (w[u >> 1] & 0xffff0000u) : (w[u >> 1] << 16));
-                pv.v[u] = from_f32<PD>(muon_apply_value<PD>(to_f32(pv.v[u]), uf, wdf, al, dwd, rp));
-            }
-            vstore<PD, 8>(P, e, pv);
-        };
-        if (fa->transposed) {  // parameter rows are rows of U^T: T row c -> row n0 + c
+        for (int i = 0; i < kChunks; ++i) {
+            const int q = threadIdx.x + TT * i;
+            // transposed: parameter rows are rows of U^T, T row c -> row n0 + c;
+            // else rows of U, gathered from two column chunks of T as C below
+            e[i] = tr ? (int64_t)(n0 + (q >> 5)) * g.M + m0 + (q & 31) * 8
+                      : (int64_t)(m0 + (q & 31) + 32 * (q >> 10)) * g.N + n0 + ((q >> 5) & 31) * 8;
+            pv[i] = vload<PD, 8>(P, e[i]);
+        }
 #pragma unroll
-            for (int i = 0; i < kChunks; ++i) {
-                const int q = threadIdx.x + TT * i;
-                const int c = q >> 5, r8 = (q & 31) * 8;
-                const uint2* t = reinterpret_cast<const uint2*>(T + c * LDT + r8);
+        for (int i = 0; i < kChunks; ++i) {
+            const int q = threadIdx.x + TT * i;
+            uint32_t w[4];
+            if (tr) {
+                const uint2* t = reinterpret_cast<const uint2*>(T + (q >> 5) * LDT + (q & 31) * 8);
                 const uint2 lo = t[0], hi = t[1];
-                const uint32_t w[4] = {lo.x, lo.y, hi.x, hi.y};
-                update8((int64_t)(n0 + c) * g.M + m0 + r8, w);
-            }
-        } else {  // parameter rows are rows of U, gathered from two column chunks as C below
-#pragma unroll
-            for (int i = 0; i < kChunks; ++i) {
-                const int q = threadIdx.x + TT * i;
-                const int r = (q & 31) + 32 * (q >> 10), c8 = ((q >> 5) & 31) * 8;
-                const uint16_t* t = T + c8 * LDT + r;
+                w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
+            } else {
+                const uint16_t* t = T + ((q >> 5) & 31) * 8 * LDT + (q & 31) + 32 * (q >> 10);
                 uint32_t h[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) h[u] = t[u * LDT];
-                const uint32_t w[4] = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                                       h[6] | (h[7] << 16)};
-                update8((int64_t)(m0 + r) * g.N + n0 + c8, w);
+                w[0] = h[0] | (h[1] << 16); w[1] = h[2] | (h[3] << 16);
+                w[2] = h[4] | (h[5] << 16); w[3] = h[6] | (h[7] << 16);
             }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float uf = __uint_as_float((u & 1) ? (w[u >> 1] & 0xffff0000u) : (w[u >> 1] << 16));
+                pv[i].v[u] = from_f32<PD>(muon_apply_value<PD>(to_f32(pv[i].v[u]), uf, wdf, al, dwd, rp));
+            }
+            vstore<PD, 8>(P, e[i], pv[i]);
         }
         return;
     }
