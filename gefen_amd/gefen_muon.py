@@ -332,9 +332,14 @@ class _MuonPlan:
         self.stacks = stacks
         # stacks with Newton-Schulz steps apply their updates in their last product
         # (gefen_gemm_bf16_nt_batched_apply); the other tensors take gefen_muon_apply_tasks
+        # (parameters of 8-element aligned addresses, as that epilogue's vector
+        # accesses need; a stack with another parameter keeps the separate pass)
         fused = np.zeros(len(items), dtype=bool)
+        self.fuse = []
         for key, idx, _, _, _ in stacks:
-            if key[4] > 0:
+            ok = key[4] > 0 and all(items[i][1].data_ptr() % (8 * items[i][1].element_size()) == 0 for i in idx)
+            self.fuse.append(ok)
+            if ok:
                 fused[idx] = True
         self.rest = np.nonzero(~fused)[0]
         self.sumsq = sumsq
@@ -394,11 +399,11 @@ class _MuonPlan:
             # stack, with an even or zero step count): every input and result stays
             # referenced here until the launch that reads them is enqueued
             keep = []
-            for key, idx, buf, work, sum_index in self.stacks:
+            for (key, idx, buf, work, sum_index), fuse in zip(self.stacks, self.fuse):
                 coeffs, steps, eps = key[3], key[4], key[5]
                 x = buf if key[2] == torch.bfloat16 else buf.bfloat16()
                 sums = self.sumsq if sum_index is not None else None
-                if steps > 0:  # the last product updates the parameters (gefen_muon.py:47, 325-329)
+                if fuse:  # the last product updates the parameters (gefen_muon.py:47, 325-329)
                     newton_schulz_batched(x, coeffs, steps, eps, work=work, sumsq=sums, index=sum_index,
                                           apply=self.apply[idx])
                     keep.append(x)

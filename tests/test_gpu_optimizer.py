@@ -280,3 +280,41 @@ def test_cached_muon_plan_matches_rebuilt_tables(host_checks, monkeypatch):
                                               err_msg="step {} {} {}".format(step, key, i))
             assert oa.state[pa[i]]["step"] == ob.state[pb[i]]["step"]
     assert planned >= 7  # the plan served most steps
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_muon_plan_with_unaligned_parameters_keeps_the_separate_update(dtype):
+    """Parameters at addresses that are not 8-element aligned (views into a flat
+    buffer) cannot take the update fused into the last Newton-Schulz product: the
+    cached plan applies it with the separate pass instead, and every step equals
+    the same optimizer on aligned copies of the parameters (which fuses), bit for
+    bit."""
+    from gefen_amd.gefen_muon import GefenMuon
+
+    shapes = [(256, 512), (512, 256)]
+    gen = torch.Generator().manual_seed(11)
+    init = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    flat = torch.zeros(sum(t.numel() for t in init) + 8, dtype=dtype, device="cuda:0")
+    views, o = [], 3  # 3 elements in: no parameter is 8-element aligned
+    for t in init:
+        v = flat[o:o + t.numel()].view(t.shape)
+        v.copy_(t.to("cuda:0"))
+        views.append(torch.nn.Parameter(v))
+        o += t.numel()
+    plain = [torch.nn.Parameter(t.to("cuda:0")) for t in init]
+    assert all(v.data_ptr() % (8 * v.element_size()) for v in views)
+    oa = GefenMuon([("u{}".format(i), v) for i, v in enumerate(views)], lr=0.02, weight_decay=0.01)
+    ob = GefenMuon([("a{}".format(i), v) for i, v in enumerate(plain)], lr=0.02, weight_decay=0.01)
+    for step in range(1, 5):
+        for i, s in enumerate(shapes):
+            g = (torch.randn(s, generator=gen) * 1e-3).to(dtype).to("cuda:0")
+            views[i].grad = g
+            plain[i].grad = g.clone()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        if step > 1:
+            assert oa._plan is not None and not any(oa._plan.fuse)
+            assert ob._plan is not None and all(ob._plan.fuse)
+        for i in range(len(shapes)):
+            np.testing.assert_array_equal(gu.to_np(views[i]), gu.to_np(plain[i]), err_msg="step {} p{}".format(step, i))
