@@ -159,9 +159,13 @@ def test_gefen_muon_matches_reference_trajectory(name):
                 ours = orc.to_f32(gu.to_np(t).reshape(-1), dtype) - p0
                 ref = orc.to_f32(tu.bits(data["p{}/step{}".format(i, step)]).reshape(-1), dtype) - p0
                 # Newton-Schulz: five rounds of bf16 GEMMs whose fp32 accumulation order differs
-                # from the reference's CPU BLAS; the accumulated update agrees to a few percent
-                tol = 0.05 if dtype != "f32" else 0.03
+                # from the reference's CPU BLAS (every product is held to 1 bf16 ulp of the
+                # reference's in test_gpu_ns_parity.py); the accumulated update agrees to a few
+                # percent (measured at most 4.1% for bf16 parameters, at step 2 where a one-ulp
+                # parameter difference is large against the update, and 1.2% for float32)
+                tol = 0.05 if dtype != "f32" else 0.015
                 rel = np.linalg.norm(ours - ref) / max(np.linalg.norm(ref), 1e-30)
+                print("{} p{} step {}: relative update error {:.3g}".format(name, i, step, rel), flush=True)
                 assert rel <= tol, "{} p{} step {}: relative update error {:.3g}".format(name, i, step, rel)
 
 
