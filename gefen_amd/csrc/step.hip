@@ -38,7 +38,7 @@ namespace gefen {
 #define GEFEN_MUON_TAB_LOG2 6  // GefenMuon row tables for lane groups of 64 lanes
 #endif
 #ifndef GEFEN_MUON_ITER
-#define GEFEN_MUON_ITER 1
+#define GEFEN_MUON_ITER 2  // two wave-units per wave: the Qwen3-1.7B momentum pass 1.58 -> 1.49 ms (3 and 4: 1.54)
 #endif
 #ifndef GEFEN_STEP_ITER_ROWS
 #define GEFEN_STEP_ITER_ROWS 1
