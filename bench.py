@@ -24,7 +24,8 @@ written into the same gradient buffers (outside the timed region).
 * other_configs (default config only, unless --headline-only): the metric's
   other named shapes, GPT-2 124M (fp32) and Llama-3 1.5B (bf16), and the
   GefenMuon Qwen3-1.7B step, each measured the same way in the same run after
-  the 8B tensors are freed (step ms, kernel roofline; no CPU baseline).
+  the 8B tensors are freed (step ms, kernel roofline, and a CPU baseline on a
+  smaller time budget).
 """
 
 from __future__ import annotations
@@ -511,7 +512,7 @@ def cpu_baseline_kernels(g_host, period_divs):
                       "thread)".format((t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3)}
 
 
-def measure(name, args, dev, with_cpu, copy_gbs=None):
+def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
     """One config's JSON object: median step() latency over args.steps timed steps
     after args.warmup untimed ones (new gradients before every step), the
     kernel roofline, and (with_cpu) the CPU baseline."""
@@ -591,11 +592,11 @@ def measure(name, args, dev, with_cpu, copy_gbs=None):
                            "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes),
                            "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
         if with_cpu:
-            out["cpu_baseline"] = cpu_baseline(opt, params)
+            out["cpu_baseline"] = cpu_baseline(opt, params, budget_s=cpu_budget_s)
     else:
         out["roofline"] = muon_ns_roofline(opt, params)
         if with_cpu:
-            out["cpu_baseline"] = cpu_baseline_muon(opt, params)
+            out["cpu_baseline"] = cpu_baseline_muon(opt, params, budget_s=cpu_budget_s)
     return out
 
 
@@ -606,7 +607,7 @@ def compact(out):
     return {"workload": out["config"]["workload"], "ms_per_step": out["value"], "p10_ms": out["p10_ms"],
             "p90_ms": out["p90_ms"], "first_step_ms": out["first_step_ms"], "dtype": out["dtype"],
             "vs_readme": out["vs_baseline"], "periods": out["config"]["periods"],
-            "roofline": {k: r[k] for k in keep if k in r}}
+            "roofline": {k: r[k] for k in keep if k in r}, "cpu_baseline": out.get("cpu_baseline")}
 
 
 def main():
@@ -647,7 +648,8 @@ def main():
             gc.collect()
             torch.cuda.empty_cache()
             try:
-                others[name] = compact(measure(name, args, dev, False, out["roofline"].get("copy_kernel_gbs")))
+                others[name] = compact(measure(name, args, dev, not args.no_cpu_baseline,
+                                               out["roofline"].get("copy_kernel_gbs"), cpu_budget_s=5.0))
             except Exception as e:  # the headline line is printed regardless
                 others[name] = {"error": repr(e)[:300]}
         out["other_configs"] = others
