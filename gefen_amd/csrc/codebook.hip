@@ -26,11 +26,16 @@ __device__ __forceinline__ float f_dec(int32_t o) {
     return o >= 0 ? __uint_as_float((uint32_t)o) : __uint_as_float(0x80000000u | (uint32_t)(-o));
 }
 
+// byte offsets of the fields the GPU tests read from a prepared table
+static_assert(offsetof(CodebookTables, bucket_fine) == 6176 && offsetof(CodebookTables, max_probe) == 22588 &&
+                  offsetof(CodebookTables, max_probe_fine) == 22592 && offsetof(CodebookTables, nb16) == 22608,
+              "codebook table layout");
+
 __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restrict__ cb, int K,
                                                           CodebookTables* __restrict__ T) {
     __shared__ float thr[260];
-    __shared__ uint16_t bk[4100];
-    __shared__ int probe_max;
+    __shared__ uint16_t bk[kFineCells + 1];
+    __shared__ int probe_max, probe_max_fine;
     const int t = threadIdx.x;
     T->cb[t] = t < K ? cb[t] : __builtin_inff();
     if (t == 0) T->K = K;
@@ -57,36 +62,47 @@ __global__ __launch_bounds__(256) void k_prepare_codebook(const float* __restric
         T->thr[k] = v;
     }
     __syncthreads();
-    // bucket[e] = #{k in 1..K-1 : thr[k] < -1 + e/2048}
-    for (int e = t; e < 4100; e += 256) {
-        uint16_t c = 0;
-        if (e <= 4096) {
-            const float edge = -1.0f + (float)e * 0.00048828125f;
-            int lo = 1, hi = K;  // first k in [1, K) with thr[k] >= edge
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (thr[mid] < edge) lo = mid + 1; else hi = mid;
-            }
-            c = (uint16_t)(lo - 1);
+    // bucket_fine[e] = #{k in 1..K-1 : thr[k] < -1 + e/4096}; bucket[e] = bucket8[e] = bucket_fine[2e]
+    for (int e = t; e <= kFineCells; e += 256) {
+        const float edge = -1.0f + (float)e * 0.000244140625f;  // exact: a multiple of 2^-12
+        int lo = 1, hi = K;  // first k in [1, K) with thr[k] >= edge
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (thr[mid] < edge) lo = mid + 1; else hi = mid;
         }
-        T->bucket[e] = c;
-        T->bucket8[e] = (uint8_t)c;  // c <= K - 1 <= 255
+        const uint16_t c = (uint16_t)(lo - 1);
+        T->bucket_fine[e] = (uint8_t)c;  // c <= K - 1 <= 255
+        if (!(e & 1)) {
+            T->bucket[e >> 1] = c;
+            T->bucket8[e >> 1] = (uint8_t)c;
+        }
         bk[e] = c;
     }
-    if (t < 12) T->bucket8[4100 + t] = 0;
-    if (t == 0) probe_max = 0;
+    for (int e = kFineCells + 1 + t; e < kFineBytes; e += 256) T->bucket_fine[e] = 0;
+    if (t < kBucket8Bytes - 4097) T->bucket8[4097 + t] = 0;
+    if (t < 3) T->bucket[4097 + t] = 0;
+    if (t == 0) probe_max = probe_max_fine = 0;
     __syncthreads();
     // a search from bucket b (one below x's bucket) meets the thresholds in
     // [edge_b, edge_b+2); past the last edges it meets every finite one left
-    int worst = 0;
-    for (int b = t; b <= 4096; b += 256) {
-        const int hi = (b + 2 <= 4096) ? (int)bk[b + 2] : (K - 1);
+    int worst = 0, worst_fine = 0;
+    for (int b = t; b <= kFineCells; b += 256) {
+        const int hi = (b + 2 <= kFineCells) ? (int)bk[b + 2] : (K - 1);
         const int n = hi - (int)bk[b];
-        worst = n > worst ? n : worst;
+        worst_fine = n > worst_fine ? n : worst_fine;
+        if (!(b & 1)) {
+            const int hc = (b + 4 <= kFineCells) ? (int)bk[b + 4] : (K - 1);
+            const int nc = hc - (int)bk[b];
+            worst = nc > worst ? nc : worst;
+        }
     }
     atomicMax(&probe_max, worst);
+    atomicMax(&probe_max_fine, worst_fine);
     __syncthreads();
-    if (t == 0) T->max_probe = (bk[0] != 0) ? 1 << 20 : probe_max;
+    if (t == 0) {
+        T->max_probe = (bk[0] != 0) ? 1 << 20 : probe_max;
+        T->max_probe_fine = (bk[0] != 0) ? 1 << 20 : probe_max_fine;
+    }
     // nb16: #{k in 1..K-1 : thr[k] < x} for the bf16 values x of the table
     for (int i = t; i < kNb16Bytes; i += 256) {
         uint8_t c = 0;

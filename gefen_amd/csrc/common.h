@@ -161,10 +161,17 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 //            The nearest index of a non-NaN x is #{k in 1..K-1 : thr[k] < x}.
 //   bucket[e] for e = 0..4096: #{k : thr[k] < -1 + e/2048}.
 //   max_probe: most thresholds a search started one bucket low can meet before
-//            reaching x (0 if thresholds lie below -1); <= 2 lets the kernels
-//            use the fixed two-probe search.
+//            reaching x (1 << 20 if thresholds lie below -1); <= 2 lets the
+//            kernels use the fixed two-probe search.
 //   bucket8  the same counts as bytes (every count is <= 255), padded with zeros
 //            to 4112 entries: the compact copy the step kernels keep in LDS.
+//   bucket_fine, max_probe_fine: the same on a grid twice as fine,
+//            bucket_fine[e] = #{k : thr[k] < -1 + e/4096} for e = 0..8192 as
+//            bytes, padded with zeros to 8208 entries; max_probe_fine <= 1 lets
+//            the 16-bit parameter step kernels search with a single probe.
+constexpr int kBucket8Bytes = 4112;
+constexpr int kFineCells = 8192;  // cells of width 2^-12 over [-1, 1]
+constexpr int kFineBytes = 8208;
 //   nb16[i]  the nearest index of the bf16 value with bits kNb16Lo + i (i < kNb16Side)
 //            at entry kNb16Side + i, and of its negative at entry kNb16Side - 1 - i
 //            (so the entry is kNb16Side + (i ^ s) with s = 0 or -1 from the sign
@@ -176,11 +183,13 @@ constexpr int kNb16Bytes = (2 * kNb16Side + 15) / 16 * 16;
 struct CodebookTables {
     float cb[256];
     float thr[260];
-    uint8_t bucket8[4112];
+    uint8_t bucket8[kBucket8Bytes];
+    uint8_t bucket_fine[kFineBytes];
     uint16_t bucket[4100];
     int32_t K;
     int32_t max_probe;
-    int32_t pad[2];
+    int32_t max_probe_fine;
+    int32_t pad;
     alignas(16) uint8_t nb16[kNb16Bytes];
 };
 
@@ -222,13 +231,15 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t v, int width) {
 }
 
 // Nearest codebook index of x with at most two threshold probes in the common
-// case.  The bucket is taken one below floor((x + 1) * 2048) so that the fma's
-// rounding can only move it down; its count of thresholds < edge is <= the
-// answer, and the remaining thresholds in [edge, x) are counted by probing.
-template <typename B>
-__device__ __forceinline__ int nearest_fast(float x, const float* thr, const B* bucket, int K) {
-    float y = __builtin_fmaf(x, 2048.0f, 2048.0f);
-    y = fminf(fmaxf(y, 1.0f), 4097.0f);
+// case, from bucket8 (FINE: bucket_fine).  The bucket is taken one below
+// floor((x + 1) * cells / 2) so that the fma's rounding can only move it down;
+// its count of thresholds < edge is <= the answer, and the remaining thresholds
+// in [edge, x) are counted by probing.
+template <bool FINE>
+__device__ __forceinline__ int nearest_fast(float x, const float* thr, const uint8_t* bucket, int K) {
+    constexpr float kHalf = FINE ? 4096.0f : 2048.0f;
+    float y = __builtin_fmaf(x, kHalf, kHalf);
+    y = fminf(fmaxf(y, 1.0f), 2.0f * kHalf + 1.0f);
     const int b = (int)y - 1;
     int k = (x < -1.0f) ? 0 : (int)bucket[b];
     k += (thr[k + 1] < x) ? 1 : 0;  // thr[K] = +inf stops every probe at K - 1

@@ -108,24 +108,31 @@ struct StepBatch {
 };
 static_assert(sizeof(StepBatch) <= 4000, "kernel arguments are limited to 4 KB");
 
-// LDS copy of the codebook tables (6 KB): the codebook rounded to the parameter
-// dtype, the thresholds and the byte bucket index.
+// LDS copy of the codebook tables (6 KB; FINE: 10 KB): the codebook rounded to
+// the parameter dtype, the thresholds and the byte bucket index (bucket8; FINE:
+// bucket_fine, for a one-probe search).
+template <bool FINE>
 struct alignas(16) LdsTables {
     float thr[260];
-    uint8_t bucket[4112];
+    uint8_t bucket[FINE ? kFineBytes : kBucket8Bytes];
     float cbd[256];
 };
 static_assert(offsetof(CodebookTables, thr) % 16 == 0 && offsetof(CodebookTables, bucket8) % 16 == 0 &&
-                  offsetof(CodebookTables, nb16) % 16 == 0,
+                  offsetof(CodebookTables, bucket_fine) % 16 == 0 && offsetof(CodebookTables, nb16) % 16 == 0,
               "codebook tables must allow 16-byte copies");
 
-// The LDS tables are 386 16-byte pieces: thr and bucket8 follow each other in
-// CodebookTables (pieces 64..385 there), the codebook is pieces 0..63.  Every
-// piece of a thread is loaded before any is stored, so a workgroup waits for
-// one round trip to L2, not one per table.
-static_assert(offsetof(CodebookTables, thr) == 1024 && offsetof(CodebookTables, bucket8) == 2064 &&
-                  sizeof(LdsTables) == 386 * 16 && offsetof(LdsTables, bucket) == 65 * 16 &&
-                  offsetof(LdsTables, cbd) == 322 * 16,
+// The LDS tables are 16-byte pieces: thr (65 pieces, from piece 64 of
+// CodebookTables), the bucket (257 pieces of bucket8 right after thr, or 513 of
+// bucket_fine from piece 386) and the codebook (pieces 0..63).  Every piece of a
+// thread is loaded before any is stored, so a workgroup waits for one round
+// trip to L2, not one per table.
+constexpr int kThrPieces = 65;
+template <bool FINE> constexpr int bucket_pieces() { return FINE ? kFineBytes / 16 : kBucket8Bytes / 16; }
+static_assert(offsetof(CodebookTables, thr) == 64 * 16 && offsetof(CodebookTables, bucket8) == (64 + kThrPieces) * 16 &&
+                  offsetof(CodebookTables, bucket_fine) == 386 * 16 && sizeof(LdsTables<false>) == 386 * 16 &&
+                  sizeof(LdsTables<true>) == 642 * 16 && offsetof(LdsTables<true>, bucket) == kThrPieces * 16 &&
+                  offsetof(LdsTables<false>, cbd) == (kThrPieces + 257) * 16 &&
+                  offsetof(LdsTables<true>, cbd) == (kThrPieces + 513) * 16,
               "table layout");
 
 // Period-one stepsize of a bf16 state from a 384-entry square-root table
@@ -134,12 +141,15 @@ static_assert(offsetof(CodebookTables, thr) == 1024 && offsetof(CodebookTables, 
 constexpr int kRootTab = 384;
 
 // NB16: also copy the bf16 nearest-index table (CodebookTables::nb16) to nb16_lds.
-template <typename D, int NT, bool NB16 = false>
-__device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* T, int& K,
+template <typename D, int NT, bool NB16 = false, bool FINE>
+__device__ __forceinline__ void load_tables(LdsTables<FINE>& L, const CodebookTables* T, int& K,
                                             const float* root = nullptr, float* root_lds = nullptr,
                                             uint8_t* nb16_lds = nullptr) {
     using U4 = RawVec<16>::type;
-    constexpr int kPieces = 386, kPer = (kPieces + NT - 1) / NT;
+    constexpr int kThrBucketPieces = kThrPieces + bucket_pieces<FINE>();
+    constexpr int kPieces = kThrBucketPieces + 64, kPer = (kPieces + NT - 1) / NT;
+    // bucket_fine starts at piece 386, not right after thr
+    constexpr int kFineShift = FINE ? (int)(offsetof(CodebookTables, bucket_fine) / 16) - kThrPieces - 64 : 0;
     constexpr int kRootPieces = kRootTab * 4 / 16;
     constexpr int kNbPieces = kNb16Bytes / 16, kNbPer = NB16 ? (kNbPieces + NT - 1) / NT : 0;
     static_assert(NT >= kRootPieces, "one root-table piece per thread");
@@ -154,7 +164,8 @@ __device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* 
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
         const int q = threadIdx.x + r * NT;
-        if (q < kPieces) v[r] = src[q < 322 ? q + 64 : q - 322];
+        if (q < kPieces)
+            v[r] = src[q < kThrPieces ? q + 64 : (q < kThrBucketPieces ? q + 64 + kFineShift : q - kThrBucketPieces)];
     }
 #pragma unroll
     for (int r = 0; r < kNbPer; ++r) {
@@ -171,7 +182,7 @@ __device__ __forceinline__ void load_tables(LdsTables& L, const CodebookTables* 
     for (int r = 0; r < kPer; ++r) {
         const int q = threadIdx.x + r * NT;
         if (q < kPieces) {
-            if (q >= 322) {
+            if (q >= kThrBucketPieces) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) v[r][c] = __float_as_uint(round_to<D>(__uint_as_float(v[r][c])));
             }
@@ -247,27 +258,44 @@ __device__ __forceinline__ float root_stepsize(float h, const StepTask& T) {
     return __builtin_fmaf(e, r, r) * T.inv_bc1;
 }
 
+// Bucket one below x's (an fma rounding up can only reach x's own bucket),
+// clamped to the grid of bucket8 (FINE: bucket_fine): for finite x, the bucket
+// counts the thresholds below x but at most max_probe (max_probe_fine) of them.
+template <bool FINE>
+__device__ __forceinline__ int bucket_below(float x) {
+    constexpr float kHalf = FINE ? 4096.0f : 2048.0f;
+    float y = __builtin_fmaf(x, kHalf, kHalf - 1.0f);  // (x + 1) * cells / 2 - 1, rounded once
+    y = fminf(fmaxf(y, 0.0f), 2.0f * kHalf);
+    return (int)y;
+}
+
 // Nearest index with at most two threshold probes (max_probe <= 2): one
 // ds_read2 of thr[k+1], thr[k+2] after the bucket lookup.
+template <bool FINE>
 __device__ __forceinline__ int nearest_two_probe(float x, const float* thr, const uint8_t* bucket) {
-    float y = __builtin_fmaf(x, 2048.0f, 2047.0f);  // (x + 1) * 2048 - 1, rounded once
-    y = fminf(fmaxf(y, 0.0f), 4096.0f);
-    int k = bucket[(int)y];
+    int k = bucket[bucket_below<FINE>(x)];
     const float t1 = thr[k + 1], t2 = thr[k + 2];
     k += (t1 < x ? 1 : 0) + (t2 < x ? 1 : 0);
     return k;
 }
 
+// Nearest index with one threshold probe (max_probe_fine <= 1).
+__device__ __forceinline__ int nearest_one_probe(float x, const float* thr, const uint8_t* bucket_fine) {
+    const int k = bucket_fine[bucket_below<true>(x)];
+    return k + (thr[k + 1] < x ? 1 : 0);
+}
+
 // Second sweep of a row: quantise, dequantise, update p.  QROUND: the
 // dequantised update cb[idx]*mag is rounded to D (param dtype == state dtype)
-// or kept in fp32 (fp32 state).  FAST: the block magnitude is finite and
-// positive and the two-probe search is exact.  Every lane computes all R
+// or kept in fp32 (fp32 state).  PROBES 1 or 2: the block magnitude is finite
+// and positive and the search with that many probes is exact (0: the general
+// search).  Every lane computes all R
 // vectors (out-of-row vectors hold a copy of the row's last vector); only
 // in-row vectors of active rows are stored.  WD: weight decay
 // (gefen.py:1280-1281) is applied to the parameter first.  root: the LDS
 // square-root table of a period-one bf16 state, or nullptr.
-template <typename D, typename S, int W, int R, bool P1, bool TAB, bool FAST, bool WD, typename UF>
-__device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& L, const float* utab,
+template <typename D, typename S, int W, int R, bool P1, bool TAB, int PROBES, bool WD, bool FINE, typename UF>
+__device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables<FINE>& L, const float* utab,
                                             const float* root, const UF& upd_of, const Vec<D, W> (&gv)[R],
                                             const Vec<D, W> (&pv)[R], const Vec<S, W> (&vv)[R], uint8_t* idx, D* p,
                                             S* vm, uint32_t base, int lir, int lpr, bool active, int K, float mn,
@@ -312,17 +340,20 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             int k;
-            if (FAST) {
-                k = nearest_two_probe(div_by_block(upd_of(j, w), rb), L.thr, L.bucket);
+            if constexpr (PROBES == 1) {
+                static_assert(FINE, "a single probe needs the fine bucket");
+                k = nearest_one_probe(div_by_block(upd_of(j, w), rb), L.thr, L.bucket);
+            } else if constexpr (PROBES == 2) {
+                k = nearest_two_probe<FINE>(div_by_block(upd_of(j, w), rb), L.thr, L.bucket);
             } else {
                 const bool plain = (mn > 0.0f) && (mn < __builtin_inff());
                 const float uj = upd_of(j, w);
                 const float x = plain ? div_by_block(uj, rb) : ((mn > 0.0f) ? uj / mn : 0.0f);
-                k = nearest_fast(x, L.thr, L.bucket, K);
+                k = nearest_fast<FINE>(x, L.thr, L.bucket, K);
             }
             io.v[w] = (uint8_t)k;
             float u;
-            if (TAB && !P1 && FAST) {
+            if (TAB && !P1 && PROBES > 0) {
                 u = utab[k];
             } else {
                 float q = L.cbd[k] * mn;
@@ -356,7 +387,11 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables& 
 template <typename D, typename S, int W, int R, bool P1, bool TAB>
 __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) {
     constexpr bool kRoot = P1 && std::is_same<S, bf16_t>::value;
-    __shared__ LdsTables L;
+    // 16-bit parameters search the fine bucket with one probe where the codebook
+    // allows; fp32 kernels keep the 6 KB tables, which leave them one more
+    // workgroup per CU
+    constexpr bool kFine = sizeof(D) == 2;
+    __shared__ LdsTables<kFine> L;
     __shared__ float row_tab[TAB ? kStepWaves : 1][TAB ? 2 : 1][2][256];
     __shared__ __attribute__((aligned(16))) float root_lds[kRoot ? kRootTab : 4];
     // every task of a launch has the same stepsize table (flush_steps)
@@ -364,7 +399,8 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
     const float* root = root_src ? root_lds : nullptr;  // uniform
     int K;
     load_tables<D, kStepThreads>(L, B.tables, K, root_src, root_lds);
-    const bool two_probe = B.tables->max_probe <= 2;
+    const int max_probe = kFine ? B.tables->max_probe_fine : B.tables->max_probe;
+    const bool two_probe = max_probe <= 2, one_probe = kFine && max_probe <= 1;
     const int ti = find_task(B.wg_begin, B.ntasks);
     const StepTask T = B.t[ti];
 
@@ -489,15 +525,19 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-#define GEFEN_SWEEP2(FAST, WD)                                                                                 \
-    step_sweep2<D, S, W, R, P1, TAB, FAST, WD>(T, L, utab, root, upd_of, gv, pv, vv, idx, p, vm, base, lir, lpr, active, K, \
-                                               mn, rb, ss)
+#define GEFEN_SWEEP2(PROBES, WD)                                                                                 \
+    step_sweep2<D, S, W, R, P1, TAB, PROBES, WD>(T, L, utab, root, upd_of, gv, pv, vv, idx, p, vm, base, lir, lpr, active, \
+                                                 K, mn, rb, ss)
+        // (one_probe is false without the fine bucket: kFine ? 1 : 2 only keeps
+        // the single-probe sweep from being instantiated there)
         if (T.do_wd) {
-            if (fast) GEFEN_SWEEP2(true, true);
-            else GEFEN_SWEEP2(false, true);
+            if (fast && one_probe) GEFEN_SWEEP2(kFine ? 1 : 2, true);
+            else if (fast) GEFEN_SWEEP2(2, true);
+            else GEFEN_SWEEP2(0, true);
         } else {
-            if (fast) GEFEN_SWEEP2(true, false);
-            else GEFEN_SWEEP2(false, false);
+            if (fast && one_probe) GEFEN_SWEEP2(kFine ? 1 : 2, false);
+            else if (fast) GEFEN_SWEEP2(2, false);
+            else GEFEN_SWEEP2(0, false);
         }
 #undef GEFEN_SWEEP2
     }
@@ -508,7 +548,7 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
 // (P > 1 only): one workgroup per row, the second sweep re-reads g and idx.
 template <typename D, typename S>
 __global__ __launch_bounds__(kThreads) void k_gefen_step_long(const StepBatch B) {
-    __shared__ LdsTables L;
+    __shared__ LdsTables<false> L;
     __shared__ float red_mx[4], red_sum[4];
     int K;
     load_tables<D, kThreads>(L, B.tables, K);
@@ -562,7 +602,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step_long(const StepBatch B)
         const float cur = L.cbd[idx[base + j]] * mold;
         const float u = __builtin_fmaf(T.b1c, gf - cur, cur);
         const float x = (mn > 0.0f) ? u / mn : 0.0f;
-        const int k = nearest_fast(x, L.thr, L.bucket, K);
+        const int k = nearest_fast<false>(x, L.thr, L.bucket, K);
         idx[base + j] = (uint8_t)k;
         float q = L.cbd[k] * mn;
         if (QROUND) q = round_to<D>(q);
@@ -677,7 +717,7 @@ template <typename D, typename S, int W, int R, bool TAB>
 __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     constexpr bool kNb = std::is_same<D, bf16_t>::value;  // bf16 quotients: the nb16 table
     constexpr bool kPk = kNb && W % 2 == 0;                // bf16 pairs: packed conversions
-    __shared__ LdsTables L;
+    __shared__ LdsTables<false> L;
     __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
     __shared__ __attribute__((aligned(16))) uint8_t nb16[kNb ? kNb16Bytes : 16];
     int K;
@@ -839,17 +879,17 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
                 if (__builtin_amdgcn_ballot_w64(miss) != 0 && miss) {
 #pragma unroll
                     for (int w = 0; w < W; ++w)
-                        kw[w] = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
+                        kw[w] = nearest_two_probe<false>(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
                 }
             } else {
 #pragma unroll
                 for (int w = 0; w < W; ++w) {
                     if (fast) {
-                        kw[w] = nearest_two_probe(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
+                        kw[w] = nearest_two_probe<false>(round_to<D>(div_by_block(mu[j][w], rb)), L.thr, L.bucket);
                     } else {
                         float x = round_to<D>(mu[j][w] / clamped);  // div_
                         if (ms <= 0.0f) x = 0.0f;                   // masked_fill_(mag <= 0)
-                        kw[w] = nearest_fast(x, L.thr, L.bucket, K);
+                        kw[w] = nearest_fast<false>(x, L.thr, L.bucket, K);
                     }
                 }
             }
@@ -908,7 +948,7 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
 
 template <typename D, typename S>
 __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
-    __shared__ LdsTables L;
+    __shared__ LdsTables<false> L;
     __shared__ float red_mx[4];
     int K;
     load_tables<D, kThreads>(L, B.tables, K);
@@ -945,7 +985,7 @@ __global__ __launch_bounds__(kThreads) void k_muon_long(const MuonBatch B) {
         const float m1 = round_to<D>(__builtin_fmaf(T.w, gf - m0, m0));
         float x = round_to<D>(m1 / clamped);
         if (ms <= 0.0f) x = 0.0f;
-        const int k = nearest_fast(x, L.thr, L.bucket, K);
+        const int k = nearest_fast<false>(x, L.thr, L.bucket, K);
         idx[base + j] = (uint8_t)k;
         const float q = round_to<D>(L.cbd[k] * ms);
         const D o = from_f32<D>(muon_out<D, S>(q, gf, T));
@@ -1002,7 +1042,7 @@ __device__ __forceinline__ float packed_row_max(float mx, float* red) {
 // Gefen update with a given stepsize or given vmean (rows of `rowlen`), packed indices.
 template <typename D, typename S, int G>
 __global__ __launch_bounds__(kThreads) void k_gefen_step_packed(const StepBatch B) {
-    __shared__ LdsTables L;
+    __shared__ LdsTables<false> L;
     __shared__ float red[4];
     int K;
     load_tables<D, kThreads>(L, B.tables, K);
@@ -1044,7 +1084,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step_packed(const StepBatch 
         auto update = [&](int64_t e, uint32_t old) -> int {
             const float u = momentum(e, old);
             const float x = (mn > 0.0f) ? u / mn : 0.0f;
-            const int k = nearest_fast(x, L.thr, L.bucket, K);
+            const int k = nearest_fast<false>(x, L.thr, L.bucket, K);
             float q = L.cbd[k] * mn;
             if (QROUND) q = round_to<D>(q);
             const float uu = (q * ss) * T.lr;
@@ -1067,7 +1107,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step_packed(const StepBatch 
 // GefenMuon quantised momentum (as k_muon_long), packed indices.
 template <typename D, typename S, int G>
 __global__ __launch_bounds__(kThreads) void k_muon_packed(const MuonBatch B) {
-    __shared__ LdsTables L;
+    __shared__ LdsTables<false> L;
     __shared__ float red[4];
     int K;
     load_tables<D, kThreads>(L, B.tables, K);
@@ -1107,7 +1147,7 @@ __global__ __launch_bounds__(kThreads) void k_muon_packed(const MuonBatch B) {
         auto requant = [&](int64_t e, uint32_t old) -> int {
             float x = round_to<D>(lerped(e, old) / clamped);
             if (ms <= 0.0f) x = 0.0f;
-            const int k = nearest_fast(x, L.thr, L.bucket, K);
+            const int k = nearest_fast<false>(x, L.thr, L.bucket, K);
             const float q = round_to<D>(L.cbd[k] * ms);
             out[e] = from_f32<D>(muon_out<D, S>(q, to_f32(g[e]), T));
             return k;

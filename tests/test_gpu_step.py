@@ -146,8 +146,10 @@ def _run_case(name, dt, sdt, n, period, wd, e_lo=-14, e_hi=-4, b2=0.999, eps=1e-
 
 
 def _special_codebook(kind):
-    if kind == "dense":   # codewords closer than the 4096-bucket width: the probing loop path
+    if kind == "dense":   # thresholds ~1.9 cells of 2^-12 apart: the two-probe search
         cb = np.concatenate([[-1.0], np.linspace(-0.06, 0.06, 254), [1.0]]).astype(np.float32)
+    elif kind == "denser":  # several thresholds per cell: the probing loop path
+        cb = np.concatenate([[-1.0], np.linspace(-0.02, 0.02, 254), [1.0]]).astype(np.float32)
     elif kind == "wide":  # entries beyond [-1, 1] (a loaded, not learned, codebook)
         cb = np.sort(np.concatenate([np.linspace(-2.0, 2.0, 200), np.linspace(-0.1, 0.1, 56)])).astype(np.float32)
     else:                 # padded codebook with repeated entries
@@ -155,11 +157,12 @@ def _special_codebook(kind):
     return np.ascontiguousarray(cb)
 
 
-@pytest.mark.parametrize("kind", ["dense", "wide", "repeated"])
+@pytest.mark.parametrize("kind", ["dense", "denser", "wide", "repeated"])
 @pytest.mark.parametrize("dt,period", [("bf16", 2048), ("bf16", 256), ("f32", 96), ("bf16", 1)])
 def test_step_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, period):
-    """General search path (many thresholds per bucket, thresholds below -1,
-    duplicate codewords) and rows whose magnitude is 0, inf or NaN."""
+    """The two-probe search (dense), the general search (many thresholds per
+    cell, thresholds below -1, duplicate codewords) and rows whose magnitude is
+    0, inf or NaN."""
     print("case", kind, dt, period, flush=True)
     cb = _special_codebook(kind)
     n = (period if period > 1 else 256) * 16
@@ -345,7 +348,7 @@ def test_invalid_arguments_raise_value_error():
         _lib.check(lib.gefen_step_tasks(task.ctypes.data, 1, tables.data_ptr(), gu.stream()))
 
 
-@pytest.mark.parametrize("kind", ["dense", "wide", "repeated"])
+@pytest.mark.parametrize("kind", ["dense", "denser", "wide", "repeated"])
 @pytest.mark.parametrize("dt,block", [("bf16", 2048), ("bf16", 256), ("f32", 96), ("f32", 1024)])
 def test_muon_momentum_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, block):
     """GefenMuon momentum through gefen_muon_tasks: general search path, row tables
@@ -388,9 +391,41 @@ def test_muon_momentum_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, 
 
 
 # CodebookTables (gefen_amd/csrc/common.h): cb 256 f32, thr 260 f32, bucket8 4112 u8,
-# bucket 4100 u16, K, max_probe, 2 pad i32, then the 16-byte aligned bf16 table
-_NB16_OFFSET = 14400
+# bucket_fine 8208 u8, bucket 4100 u16, K, max_probe, max_probe_fine, pad i32, then
+# the 16-byte aligned bf16 table
+_BUCKET8_OFFSET, _FINE_OFFSET = 2064, 6176
+_MAX_PROBE_OFFSET = 22588  # max_probe, then max_probe_fine
+_NB16_OFFSET = 22608
 _NB16_LO, _NB16_SIDE = 0x3580, 0x3F82 - 0x3580
+
+
+@pytest.mark.parametrize("kind,probes", [("learned", 1), ("uniform", 1), ("dense", 2), ("denser", 3),
+                                         ("repeated", 3)])
+def test_codebook_tables_choose_the_search(kind, probes):
+    """bucket8[e] and bucket_fine[e] are the oracle's nearest index of the bucket
+    edges -1 + e/2048 and -1 + e/4096 (the count of thresholds below them) for
+    every e, and max_probe_fine puts each codebook on the search the 16-bit
+    parameter step kernels take for it: one probe for the learned and the
+    uniform codebook, two for thresholds ~1.9 fine cells apart, the general loop
+    (3 and more) for denser or repeated codewords.  A coarse bucket holds two
+    fine ones, so max_probe (the other kernels' choice) is never below it."""
+    print("tables", kind, flush=True)
+    if kind == "learned":
+        cb = _codebook()
+    elif kind == "uniform":
+        cb = np.linspace(-1.0, 1.0, 256).astype(np.float32)
+    else:
+        cb = _special_codebook(kind)
+    tables = gu.to_np(_tables(torch.from_numpy(cb).to("cuda:0")))
+    for off, cells in ((_BUCKET8_OFFSET, 4096), (_FINE_OFFSET, 8192)):
+        edges = (-1.0 + np.arange(cells + 1, dtype=np.float64) * (2.0 / cells)).astype(np.float32)
+        np.testing.assert_array_equal(tables[off:off + cells + 1], orc.nearest(cb, edges).astype(np.uint8))
+    max_probe, max_probe_fine = (int(v) for v in tables[_MAX_PROBE_OFFSET:_MAX_PROBE_OFFSET + 8].view(np.int32))
+    if probes < 3:
+        assert max_probe_fine == probes
+    else:
+        assert max_probe_fine >= 3
+    assert max_probe >= max_probe_fine
 
 
 @pytest.mark.parametrize("cbkind", ["learned", "zero_threshold"])
