@@ -33,7 +33,9 @@ COMMON = [
 ]
 
 LIBS = {
-    "libgefen_hip.so": ["capi.cpp", "step.hip", "codebook.hip", "period.hip", "ns_gemm.hip", "muon.hip"],
+    "libgefen_hip.so": ["capi.cpp", "step.hip", "step_inst_bf16.hip", "step_inst_f16.hip", "step_inst_f32.hip",
+                        "step_inst_bf16_f32.hip", "step_inst_f16_f32.hip", "codebook.hip", "period.hip", "ns_gemm.hip",
+                        "muon.hip"],
     "libgefen_synth.so": ["capi.cpp", "synthetic.hip"],
 }
 
@@ -52,7 +54,17 @@ def _compile(src: Path, obj: Path) -> None:
         sys.stderr.write("\n".join(msgs) + "\n")
 
 
-def build(jobs: int = 8, only=None) -> None:
+def _stale(src: Path, obj: Path) -> bool:
+    """obj is older than src or than any header of csrc/ or include/."""
+    if not obj.exists():
+        return True
+    deps = [src] + list(CSRC.glob("*.h")) + list((REPO / "include").glob("*.h"))
+    return obj.stat().st_mtime < max(d.stat().st_mtime for d in deps)
+
+
+def build(jobs: int = 8, only=None, incremental: bool = False) -> None:
+    """Compile and link every library (incremental: only objects older than
+    their source or a header are compiled again)."""
     BUILD.mkdir(exist_ok=True)
     for lib, srcs in LIBS.items():
         if only and lib not in only:
@@ -63,7 +75,8 @@ def build(jobs: int = 8, only=None) -> None:
             src = CSRC / s
             obj = BUILD / (s + ".o")
             objs.append(obj)
-            todo.append((src, obj))
+            if not incremental or _stale(src, obj):
+                todo.append((src, obj))
         with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
             list(ex.map(lambda a: _compile(*a), todo))
         out = PKG / lib
@@ -121,6 +134,8 @@ def build_host_ext() -> None:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--incremental", action="store_true",
+                    help="compile only objects older than their source or a header")
     args = ap.parse_args()
-    build(args.jobs)
+    build(args.jobs, incremental=args.incremental)
     print("built", ", ".join(list(LIBS) + ["_gefen_host", "test helpers"]))

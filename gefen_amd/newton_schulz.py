@@ -59,9 +59,18 @@ def newton_schulz_bf16(grad: torch.Tensor, coeffs: Tuple[float, float, float], s
     return x
 
 
+# The batched kernels address an operand through a buffer resource whose extent
+# is a 32-bit byte count: the Gram product reads a whole X^T [n, m] through one
+# (gefen_gram_bf16_batched rejects k * ldxt * 2 > 2^31 - 1), so a matrix of 2^30 or
+# more bf16 elements takes the one-matrix path, which forms 64-bit addresses.
+_BATCHED_MAX_BYTES = (1 << 31) - 1
+
+
 def batched_shape_ok(rows: int, cols: int) -> bool:
-    """The batched GEMM tiles m = min(rows, cols) and n = max(rows, cols) by 256."""
-    return rows > 0 and cols > 0 and rows % 256 == 0 and cols % 256 == 0
+    """The batched GEMM tiles m = min(rows, cols) and n = max(rows, cols) by 256,
+    and reads one bf16 matrix through a buffer of less than 2^31 bytes."""
+    return (rows > 0 and cols > 0 and rows % 256 == 0 and cols % 256 == 0
+            and rows * cols * 2 <= _BATCHED_MAX_BYTES)
 
 
 def gemm_nt_batched(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, out_t: torch.Tensor = None,

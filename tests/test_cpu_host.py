@@ -63,6 +63,26 @@ def test_entry_points_reject_invalid_arguments_without_a_device():
     assert lib.gefen_exact_dp_workspace_size(4096, 256) > 256 * 4097 * 12
 
 
+def test_batched_newton_schulz_shape_predicate_matches_the_byte_limit():
+    """A matrix the batched Gram product would refuse (X^T spanning 2^31 bytes or
+    more) goes to the one-matrix path: batched_shape_ok says no exactly where
+    gefen_gram_bf16_batched raises, so GefenMuon never starts a step it cannot finish."""
+    from gefen_amd import _lib
+    from gefen_amd.newton_schulz import batched_shape_ok
+
+    lib = _lib.load()
+    # 32768 x 32768 bf16 = 2^31 bytes: refused; 32768 x 32512 = 2^31 - 2^24: accepted
+    assert not batched_shape_ok(32768, 32768)
+    assert batched_shape_ok(32768, 32512) and batched_shape_ok(32512, 32768)
+    assert not batched_shape_ok(128256, 16384) and not batched_shape_ok(16384, 128256)
+    assert batched_shape_ok(2048, 6144) and not batched_shape_ok(2048, 6000)
+    for rows, cols in ((32768, 32768), (131072, 16384), (16384, 131072)):
+        m, n = min(rows, cols), max(rows, cols)
+        assert not batched_shape_ok(rows, cols)
+        with pytest.raises(ValueError, match="operand too large"):
+            _lib.check(lib.gefen_gram_bf16_batched(256, m, 0, 256, m, 0, 1, m, n, 1.0, None))
+
+
 def test_divisors_and_period_selection_match_the_oracle_restatement():
     from gefen_amd import partitioning as part
 
