@@ -15,10 +15,14 @@ written into the same gradient buffers (outside the timed region).
   timed steps (synchronised per step), steady state (steps after the first).
 * roofline: algorithmic HBM bytes of one step (p read+write, g read, 8-bit
   index read+write, per-block state read+write with the chosen periods) divided
-  by the GPU time of the fused step kernels, measured with HIP events on the
-  launch stream around ``gefen_step_tasks``.  copy_kernel_gbs: a plain 2 GiB
-  device copy (16-byte vectors) timed the same way on the same box, and
-  frac_of_copy the step kernels' bandwidth as a fraction of it.
+  by the GPU time of the step's launches inside real ``optimizer.step()`` calls
+  (each after a gradient refill), from HIP events the kept step plan records on
+  the launch stream right before its first launch and after its last (median
+  over a second pass of timed steps).  step_frac: the same bytes divided by
+  ms_per_step (host time included).  frac_back_to_back: the launches repeated
+  back to back on unchanged gradients.  copy_kernel_gbs: a plain 2 GiB device
+  copy (16-byte vectors) timed on the same box, and frac_of_copy the step's
+  bandwidth as a fraction of it.
 * cpu_baseline: the CPU oracle (C restatement of the reference CPU path,
   OpenMP) on a bounded sample of the same tensors, scaled to a full step.
 * other_configs (default config only, unless --headline-only): the metric's
@@ -31,6 +35,7 @@ written into the same gradient buffers (outside the timed region).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import gc
 import json
 import math
@@ -568,10 +573,31 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
         periods[P] = periods.get(P, 0) + 1
     out["config"]["periods"] = {str(k): v for k, v in sorted(periods.items())}
     if cfg["opt"] == "gefen":
-        # fused step kernels alone, HIP events on the launch stream
+        lib = _lib.load()
+        # the step's launches timed inside real optimizer.step() calls (each after a
+        # gradient refill, like the timed steps): the kept plan records HIP events on
+        # the launch stream right before its first launch and after its last
+        # (a second pass, so that the timed steps above carry no event records)
+        plan = opt._plan
+        if plan is None or not plan.handle:
+            raise RuntimeError("the optimizer did not keep a step plan")
+        _lib.check(lib.gefen_step_plan_time_runs(plan.handle, 1))
+        in_step = []
+        for _ in range(args.steps):
+            set_grads(step_no)
+            step_no += 1
+            opt.step()
+            if opt._plan is not plan:
+                raise RuntimeError("the step plan was rebuilt during the timed steps")
+            ms = ctypes.c_float()
+            _lib.check(lib.gefen_step_plan_last_ms(plan.handle, ctypes.byref(ms)))
+            in_step.append(ms.value)
+        _lib.check(lib.gefen_step_plan_time_runs(plan.handle, 0))
+        kms = statistics.median(in_step)
+        # the same launches back to back on unchanged gradients (the kernels' own
+        # rate at the shader clock of a busy GPU; not the reported figure)
         tasks = kernel_tasks(opt, [(n, p) for n, p in params])
         tables = opt._codebook_tables()
-        lib = _lib.load()
         stream = torch.cuda.current_stream()
         for _ in range(2):
             _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream))
@@ -582,7 +608,7 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
             _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream))
         e1.record(stream)
         torch.cuda.synchronize()
-        kms = e0.elapsed_time(e1) / reps
+        kms_b2b = e0.elapsed_time(e1) / reps
         nbytes = step_bytes(opt, params)
         achieved = nbytes / (kms * 1e-3) / 1e9
         if copy_gbs is None:
@@ -590,6 +616,9 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg, nbytes),
                            "kernel_ms_per_step": round(kms, 4), "algorithmic_bytes_per_step": int(nbytes),
+                           "step_frac": round(nbytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "kernel_ms_back_to_back": round(kms_b2b, 4),
+                           "frac_back_to_back": round(nbytes / (kms_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                            "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
         if with_cpu:
             out["cpu_baseline"] = cpu_baseline(opt, params, budget_s=cpu_budget_s)
@@ -603,7 +632,8 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
 def compact(out):
     """The figures of a further config's line that the headline line carries."""
     r = out["roofline"]
-    keep = ("bound", "achieved", "peak", "unit", "frac", "kernel_ms_per_step", "frac_of_copy")
+    keep = ("bound", "achieved", "peak", "unit", "frac", "kernel_ms_per_step", "step_frac", "frac_back_to_back",
+            "frac_of_copy")
     return {"workload": out["config"]["workload"], "ms_per_step": out["value"], "p10_ms": out["p10_ms"],
             "p90_ms": out["p90_ms"], "first_step_ms": out["first_step_ms"], "dtype": out["dtype"],
             "vs_readme": out["vs_baseline"], "periods": out["config"]["periods"],

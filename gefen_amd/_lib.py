@@ -28,6 +28,7 @@ SZ = ctypes.c_size_t
 SIGNATURES = {
     "gefen_last_error": (ctypes.c_char_p, []),
     "gefen_abi_version": (I32, []),
+    "gefen_device_allocations": (I64, []),
     "gefen_struct_size": (SZ, [I32]),
     "gefen_codebook_tables_size": (SZ, []),
     "gefen_prepare_codebook": (I32, [P, I32, P, P]),
@@ -40,6 +41,11 @@ SIGNATURES = {
     "gefen_automatic_muon_momentum": (I32, [P, I32, P, P, I32, P, I32, P, I32, I64, I64, DBL, P]),
     "gefen_step_tasks": (I32, [P, I32, P, P]),
     "gefen_step_tasks_noalloc": (I32, [P, I32, P, P]),
+    "gefen_step_plan_create": (I32, [P, I32, P, P]),
+    "gefen_step_plan_run": (I32, [P, P, I32, P]),
+    "gefen_step_plan_time_runs": (I32, [P, I32]),
+    "gefen_step_plan_last_ms": (I32, [P, P]),
+    "gefen_step_plan_destroy": (None, [P]),
     "gefen_muon_tasks": (I32, [P, I32, P, P]),
     "gefen_muon_tasks_sumsq": (I32, [P, I32, P, P, P]),
     "gefen_ns_prepare": (I32, [P, P, I32, I32, I32, DBL, P]),

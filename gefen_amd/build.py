@@ -117,7 +117,7 @@ def build_host_ext() -> None:
     torch_lib = cpp_extension.library_paths()[0]
     out = PKG / ("_gefen_host" + sysconfig.get_config_var("EXT_SUFFIX"))
     tmp = out.with_name(out.name + ".tmp")
-    cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall",
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall", "-ffp-contract=off",
            "-D_GLIBCXX_USE_CXX11_ABI={}".format(int(torch.compiled_with_cxx11_abi())),
            "-I", sysconfig.get_paths()["include"]]
     for inc in cpp_extension.include_paths():

@@ -2,10 +2,13 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "capi_internal.h"
 
 namespace {
 thread_local char g_error[512] = "";
+std::atomic<int64_t> g_allocations{0};
 }
 
 namespace gefen {
@@ -31,7 +34,19 @@ int hip_status(hipError_t e, const char* what) {
     return GEFEN_ERUNTIME;
 }
 
+hipError_t device_malloc(void** ptr, size_t bytes) {
+    g_allocations.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(ptr, bytes);
+}
+
+hipError_t device_malloc_async(void** ptr, size_t bytes, hipStream_t st) {
+    g_allocations.fetch_add(1, std::memory_order_relaxed);
+    return hipMallocAsync(ptr, bytes, st);
+}
+
 }  // namespace gefen
+
+extern "C" int64_t gefen_device_allocations(void) { return g_allocations.load(std::memory_order_relaxed); }
 
 extern "C" const char* gefen_last_error(void) { return g_error; }
 extern "C" int gefen_abi_version(void) { return 1; }

@@ -17,6 +17,11 @@ int fail_inval(const char* fmt, ...);
 // Return GEFEN_ERUNTIME with the HIP error text when e != hipSuccess.
 int hip_status(hipError_t e, const char* what);
 
+// Every device allocation of the library (pools, workspaces, temporaries) goes
+// through these, which count them for gefen_device_allocations().
+hipError_t device_malloc(void** ptr, size_t bytes);
+hipError_t device_malloc_async(void** ptr, size_t bytes, hipStream_t st);
+
 // Check the last launch of the calling thread.
 inline int launch_status(const char* what) { return hip_status(hipGetLastError(), what); }
 

@@ -553,7 +553,7 @@ struct TempTables {
     hipStream_t st = nullptr;
     int init(const float* cb, int K, hipStream_t s) {
         st = s;
-        hipError_t e = hipMallocAsync(&ptr, sizeof(CodebookTables), s);
+        hipError_t e = device_malloc_async(&ptr, sizeof(CodebookTables), s);
         if (e != hipSuccess) return hip_status(e, "hipMallocAsync(codebook tables)");
         return gefen_prepare_codebook(cb, K, ptr, reinterpret_cast<gefen_stream_t>(s));
     }

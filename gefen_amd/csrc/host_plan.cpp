@@ -185,17 +185,25 @@ class PlanCore {
     size_t size() const { return params_.size(); }
 
    private:
-    // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group.
-    // A tensor lr of another dtype than float64 with weight decay > 0 is refused:
-    // torch forms that decay factor in the tensor's dtype (the Python step applies
-    // it before the launch), where the kernel's double expression would differ.
+    // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group,
+    // the weight decay as the kernels take it.  For a float32 tensor lr with
+    // weight decay, torch forms the decay factor in float32,
+    // f = fl32(1 - fl32(lr * fl32(wd))) (gefen.py:1280-1281), while the kernels
+    // form (float)(1 - lr * wd) in double: they get wd' = (1 - f) / lr instead,
+    // for which that double expression lies within ~2^-51 (relative) of f and so
+    // rounds to f exactly (gefen.py's _kernel_weight_decay does the same).  A
+    // tensor lr of a 16-bit dtype with weight decay, lr <= 0 or f zero or not
+    // finite is refused: the Python step applies torch's factor before the launch.
     bool group_hyper(PyObject* group, std::array<double, 5>& h) {
         PyObject* keys[5] = {key_lr_, key_beta1_, key_beta2_, key_eps_, key_wd_};
-        bool lr_tensor = false;
+        int lr_kind = 0;  // 0: number or float64 tensor, 1: float32 tensor, 2: other tensor
         for (int c = 0; c < 5; ++c) {
             PyObject* v = PyDict_GetItem(group, keys[c]);
             if (!v) return false;
-            if (c == 0) lr_tensor = THPVariable_Check(v) && THPVariable_Unpack(v).scalar_type() != at::kDouble;
+            if (c == 0 && THPVariable_Check(v)) {
+                const at::ScalarType st = THPVariable_Unpack(v).scalar_type();
+                lr_kind = st == at::kDouble ? 0 : (st == at::kFloat ? 1 : 2);
+            }
             if (PyFloat_CheckExact(v)) {
                 h[c] = PyFloat_AS_DOUBLE(v);
                 continue;
@@ -208,7 +216,13 @@ class PlanCore {
             h[c] = PyFloat_AS_DOUBLE(f);
             Py_DECREF(f);
         }
-        return !(lr_tensor && h[4] > 0.0);
+        if (lr_kind == 0 || !(h[4] > 0.0)) return true;
+        if (lr_kind != 1 || !(h[0] > 0.0)) return false;
+        const volatile float prod = (float)h[0] * (float)h[4];  // volatile: each op rounded to float
+        const volatile float f = 1.0f - prod;
+        if (!std::isfinite(f) || f == 0.0f) return false;
+        h[4] = (1.0 - (double)f) / h[0];
+        return true;
     }
 
     int device_type_ = -1, device_index_ = -1;

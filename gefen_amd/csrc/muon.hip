@@ -272,7 +272,7 @@ extern "C" int gefen_ns_prepare(void* x, void* xt, int batch, int rows, int cols
     const int64_t per = (int64_t)rows * cols;
     const int nblk = (int)((per + muon::kNormChunk - 1) / muon::kNormChunk);
     void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, ((size_t)batch * nblk + batch) * sizeof(float), st);
+    hipError_t e = device_malloc_async(&ws, ((size_t)batch * nblk + batch) * sizeof(float), st);
     if (e != hipSuccess) return hip_status(e, "hipMallocAsync(norm partials)");
     float* partial = static_cast<float*>(ws);
     float* div = partial + (size_t)batch * nblk;

@@ -368,7 +368,7 @@ extern "C" int gefen_average_adjacent_log_block_mean_difference(const void* valu
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, P.total, st);
+    hipError_t e = device_malloc_async(&ws, P.total, st);
     if (e != hipSuccess) return hip_status(e, "hipMallocAsync(period workspace)");
     rc = run_scores(values, dtype, numel, divs, 1, input_is_squared ? 0 : 2, epsilon, out, static_cast<char*>(ws),
                     P, st);

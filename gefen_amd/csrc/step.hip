@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <new>
 #include <type_traits>
 #include <vector>
 
@@ -205,18 +206,9 @@ SideStream g_side[kMaxDevices];
 // Launches of fewer elements than this go to the side stream.
 constexpr int64_t kSmallLaunchElems = 1 << 20;
 
-// The side stream of the current device, or nullptr (then everything runs on
-// st): also when st belongs to another device than the current one.
-SideStream* side_stream(hipStream_t st) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-    if (st) {
-        hipDevice_t sdev = -1;
-        if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) {
-            (void)hipGetLastError();
-            return nullptr;
-        }
-    }
+// The side stream of device dev (created on first use, with dev current), or
+// nullptr when it could not be created.
+SideStream* side_stream_of(int dev) {
     SideStream& ss = g_side[dev];
     std::lock_guard<std::mutex> lock(ss.m);
     if (!ss.tried) {
@@ -231,28 +223,48 @@ SideStream* side_stream(hipStream_t st) {
     return ss.s ? &ss : nullptr;
 }
 
-// Launch every pending task.  allow_side = false keeps every launch on st (no
-// library-owned stream or event is created or used).
-int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st,
-                bool allow_side = true) {
-    // group by kernel key, up to kMaxBatch tasks per launch
-    struct Launch {
-        Key key;
-        StepBatch b;
-        int wg;
-        int64_t elems;
-    };
-    std::vector<Launch> launches;
+// The side stream of the current device, or nullptr (then everything runs on
+// st): also when st belongs to another device than the current one.
+SideStream* side_stream(hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    if (st) {
+        hipDevice_t sdev = -1;
+        if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    return side_stream_of(dev);
+}
+
+// One launch of the step kernels: a kernel key, its task table and grid.
+struct StepLaunch {
+    Key key;
+    StepBatch b;
+    int wg;
+    int64_t elems;
+};
+
+// Group the pending tasks into launches: per kernel key, up to kMaxBatch tasks
+// and one stepsize table per launch, in order of first appearance.  slot_of
+// (optional) receives, for each pending task, launch index * kMaxBatch + its
+// position in that launch's table.
+void group_launches(const std::vector<PendingStep>& pend, const CodebookTables* tables,
+                    std::vector<StepLaunch>& launches, std::vector<int>* slot_of = nullptr) {
+    launches.clear();
+    if (slot_of) slot_of->assign(pend.size(), -1);
     std::vector<bool> done(pend.size(), false);
     for (size_t i = 0; i < pend.size(); ++i) {
         if (done[i]) continue;
-        Launch L;
+        StepLaunch L;
         memset(&L.b, 0, sizeof(L.b));
         L.key = pend[i].key;
         L.b.tables = tables;
         L.elems = 0;
         int n = 0;
         int64_t wg = 0;
+        std::vector<size_t> members;
         for (size_t j = i; j < pend.size() && n < kMaxBatch; ++j) {
             if (done[j] || !(pend[j].key == pend[i].key)) continue;
             // one stepsize table per launch: workgroups load it before they find their task
@@ -262,17 +274,31 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
             L.b.wg_begin[n] = (int32_t)wg;
             wg += pend[j].task.nwg;
             L.elems += pend[j].task.nrows * pend[j].task.rowlen;
+            members.push_back(j);
             ++n;
             done[j] = true;
         }
         L.b.wg_begin[n] = (int32_t)wg;
         L.b.ntasks = n;
         L.wg = (int)wg;
-        if (wg > 0) launches.push_back(L);
+        if (wg > 0) {
+            if (slot_of)
+                for (int q = 0; q < n; ++q) (*slot_of)[members[q]] = (int)launches.size() * kMaxBatch + q;
+            launches.push_back(L);
+        }
     }
+}
+
+// Issue the launches on st; with allow_side, the launches of small tensors go
+// to the device's side stream when the call also has large ones (side: that
+// stream, or nullptr to look it up).  allow_side = false keeps every launch on
+// st (no library-owned stream or event is created or used).
+int issue_launches(const std::vector<StepLaunch>& launches, hipStream_t st, bool allow_side,
+                   SideStream* side = nullptr) {
     bool any_small = false, any_large = false;
-    for (const Launch& L : launches) (L.elems < kSmallLaunchElems ? any_small : any_large) = true;
-    SideStream* side = (allow_side && any_small && any_large) ? side_stream(st) : nullptr;
+    for (const StepLaunch& L : launches) (L.elems < kSmallLaunchElems ? any_small : any_large) = true;
+    if (!(allow_side && any_small && any_large)) side = nullptr;
+    else if (!side) side = side_stream(st);
     std::unique_lock<std::mutex> lock;
     if (side) {
         lock = std::unique_lock<std::mutex>(side->m);
@@ -280,7 +306,7 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
             return launch_status("gefen step fork");
     }
     int rc = GEFEN_OK;
-    for (const Launch& L : launches) {
+    for (const StepLaunch& L : launches) {
         hipStream_t ls = (side && L.elems < kSmallLaunchElems) ? side->s : st;
         hipError_t e = dispatch_step(L.key, L.b, L.wg, ls);
         if (e != hipSuccess) {
@@ -296,6 +322,29 @@ int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hi
         if (e2 != hipSuccess && rc == GEFEN_OK) rc = hip_status(e2, "gefen step join");
     }
     return rc;
+}
+
+// Launch every pending task.
+int flush_steps(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st,
+                bool allow_side = true) {
+    std::vector<StepLaunch> launches;
+    group_launches(pend, tables, launches);
+    return issue_launches(launches, st, allow_side);
+}
+
+// The per-step scalars of a task as the kernels take them (float), from the
+// caller's doubles: 1 - beta1, beta2, 1 - beta2, sqrt(bc2), eps, 1 / bc1, lr and
+// the weight-decay factor 1 - lr * wd.
+inline void set_step_scalars(const gefen_step_task& in, StepTask& t) {
+    t.b1c = (float)(1.0 - in.beta1);
+    t.b2 = (float)in.beta2;
+    t.omb2 = (float)(1.0 - in.beta2);
+    t.sqrt_bc2 = (float)sqrt(in.bias_correction_2);
+    t.eps = (float)in.eps;
+    t.inv_bc1 = (float)(1.0 / in.bias_correction_1);
+    t.lr = (float)in.lr;
+    t.do_wd = in.weight_decay > 0.0;
+    t.wdf = (float)(1.0 - in.lr * in.weight_decay);
 }
 
 // Build the StepTask of one tensor.  mode / stepsize select the stepsize source.
@@ -337,15 +386,7 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     t.nvec = (int32_t)std::min<int64_t>(nvec, INT32_MAX);
     t.lpr_log2 = l2;
     t.mode = mode;
-    t.b1c = (float)(1.0 - in.beta1);
-    t.b2 = (float)in.beta2;
-    t.omb2 = (float)(1.0 - in.beta2);
-    t.sqrt_bc2 = (float)sqrt(in.bias_correction_2);
-    t.eps = (float)in.eps;
-    t.inv_bc1 = (float)(1.0 / in.bias_correction_1);
-    t.lr = (float)in.lr;
-    t.do_wd = in.weight_decay > 0.0;
-    t.wdf = (float)(1.0 - in.lr * in.weight_decay);
+    set_step_scalars(in, t);
     t.nwg = task_wgs(k, t.nrows, l2, kStepWaves, k.p1 ? kIterP1 : kIterRows);
     if (t.nwg < 0) return fail_inval("tensor of %lld elements is too large for one launch", (long long)n);
     out.key = k;
@@ -368,6 +409,9 @@ constexpr size_t kLutSlot = 32768;
 static_assert(kRootSlot % 64 == 0 && kLutSlot % 64 == 0, "table slots keep 256-byte alignment");
 
 void plan_luts(const std::vector<PendingStep>& pend, LutPlan& lp) {
+    lp.keys.clear();
+    lp.off.clear();
+    lp.total = 0;
     lp.which.assign(pend.size(), -1);
     for (size_t i = 0; i < pend.size(); ++i) {
         const Key& k = pend[i].key;
@@ -434,19 +478,88 @@ struct DeviceScope {
     }
 };
 
+// Orders the calls that share a device buffer (the stepsize tables): `done` is
+// recorded on the stream of the last call after its launches, and a call on
+// another stream waits for it before rewriting the buffer.  Not used while st
+// is being captured into a graph (the graph's own edges order its nodes).
+struct StreamOrder {
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool recorded = false;
+
+    // Creates the event on first use (dev current); hipEventCreate allocates no device memory.
+    int init(int dev) {
+        if (done) return GEFEN_OK;
+        DeviceScope scope(dev);
+        hipError_t e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            done = nullptr;
+            return hip_status(e, "hipEventCreate(stepsize tables)");
+        }
+        return GEFEN_OK;
+    }
+    int wait(hipStream_t st) {
+        if (!recorded || last == st) return GEFEN_OK;
+        hipError_t e = hipStreamWaitEvent(st, done, 0);
+        return e == hipSuccess ? GEFEN_OK : hip_status(e, "hipStreamWaitEvent(stepsize tables)");
+    }
+    // After the call's launches (and the join of the side stream): rc is the
+    // call's status so far, returned unless the record itself fails.
+    int record(hipStream_t st, int rc) {
+        hipError_t e = hipEventRecord(done, st);
+        if (e == hipSuccess) {
+            recorded = true;
+            last = st;
+        } else if (rc == GEFEN_OK) {
+            rc = hip_status(e, "hipEventRecord(stepsize tables)");
+        }
+        return rc;
+    }
+};
+
+// True when st is capturing into a graph (then no event of a previous call may be waited on).
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return cs != hipStreamCaptureStatusNone;
+}
+
 // Library-owned stepsize-table memory of a device, kept between calls and grown
-// when a call needs more.  `done` is recorded on the stream of the last call
-// after its launches; a call on another stream waits for it before rewriting
-// the tables, so calls on different streams stay ordered.
+// when a call needs more; calls on different streams are ordered by `order`.
 struct LutPool {
     std::mutex m;
     float* buf = nullptr;
     size_t cap = 0;  // floats
-    hipEvent_t done = nullptr;
-    hipStream_t last = nullptr;
-    bool recorded = false;
+    StreamOrder order;
 };
 LutPool g_lut_pool[kMaxDevices];
+
+// Make the pool hold at least `floats` floats (pool.m held by the caller) and
+// order st after the pool's last call on another stream.
+int lut_pool_reserve(LutPool& pool, int dev, size_t floats, hipStream_t st) {
+    int rc = pool.order.init(dev);
+    if (rc) return rc;
+    if (pool.cap < floats) {
+        DeviceScope scope(dev);
+        if (pool.buf) {
+            if (pool.order.recorded) (void)hipEventSynchronize(pool.order.done);
+            (void)hipFree(pool.buf);
+            pool.buf = nullptr;
+            pool.cap = 0;
+        }
+        const size_t want = std::max<size_t>(floats, 4 * kLutSlot);
+        hipError_t e = device_malloc(reinterpret_cast<void**>(&pool.buf), want * sizeof(float));
+        if (e != hipSuccess) {
+            pool.buf = nullptr;
+            return hip_status(e, "hipMalloc(stepsize tables)");
+        }
+        pool.cap = want;
+    }
+    return pool.order.wait(st);
+}
 
 // Stepsize tables in the device's pool, then the step launches.
 int run_steps_pooled(std::vector<PendingStep>& pend, const CodebookTables* tables, hipStream_t st) {
@@ -458,54 +571,27 @@ int run_steps_pooled(std::vector<PendingStep>& pend, const CodebookTables* table
     if (rc) return rc;
     LutPool& pool = g_lut_pool[dev];
     std::lock_guard<std::mutex> lock(pool.m);
-    if (pool.cap < lp.total || !pool.done) {
-        DeviceScope scope(dev);
-        if (!pool.done) {
-            hipError_t e = hipEventCreateWithFlags(&pool.done, hipEventDisableTiming);
-            if (e != hipSuccess) {
-                pool.done = nullptr;
-                return hip_status(e, "hipEventCreate(stepsize tables)");
-            }
-        }
-        if (pool.cap < lp.total) {
-            if (pool.buf) {
-                if (pool.recorded) (void)hipEventSynchronize(pool.done);
-                (void)hipFree(pool.buf);
-                pool.buf = nullptr;
-                pool.cap = 0;
-            }
-            const size_t want = std::max<size_t>(lp.total, 4 * kLutSlot);
-            hipError_t e = hipMalloc(reinterpret_cast<void**>(&pool.buf), want * sizeof(float));
-            if (e != hipSuccess) {
-                pool.buf = nullptr;
-                return hip_status(e, "hipMalloc(stepsize tables)");
-            }
-            pool.cap = want;
-        }
-    }
-    if (pool.recorded && pool.last != st) {
-        hipError_t e = hipStreamWaitEvent(st, pool.done, 0);
-        if (e != hipSuccess) return hip_status(e, "hipStreamWaitEvent(stepsize tables)");
-    }
+    rc = lut_pool_reserve(pool, dev, lp.total, st);
+    if (rc) return rc;
     rc = build_luts(pend, lp, pool.buf, st);
     if (rc == GEFEN_OK) rc = flush_steps(pend, tables, st);
     // recorded after the join of the side stream: covers every launch that reads the tables
-    hipError_t e = hipEventRecord(pool.done, st);
-    if (e == hipSuccess) {
-        pool.recorded = true;
-        pool.last = st;
-    } else if (rc == GEFEN_OK) {
-        rc = hip_status(e, "hipEventRecord(stepsize tables)");
-    }
-    return rc;
+    return pool.order.record(st, rc);
 }
 
-std::mutex g_scratch_mutex;
-float* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device
+// The scratch buffer of each device: its device address (from
+// hipGetSymbolAddress, taken once with the device current) and the order of
+// the no-allocation calls that write it.
+struct ScratchSlot {
+    std::mutex m;
+    float* ptr = nullptr;
+    StreamOrder order;
+};
+ScratchSlot g_scratch[kMaxDevices];
 
-int scratch_for_device(int dev, float** out) {
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (!g_scratch_ptr[dev]) {
+// Set-up of device dev's slot on its first use (slot.m held by the caller).
+int scratch_init(ScratchSlot& slot, int dev) {
+    if (!slot.ptr) {
         DeviceScope scope(dev);
         int cur = -1;
         if (hipGetDevice(&cur) != hipSuccess || cur != dev) return fail_inval("cannot make device %d current", dev);
@@ -513,10 +599,9 @@ int scratch_for_device(int dev, float** out) {
         hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(::scratch));
         if (e != hipSuccess || !ptr) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol,
                                                        "hipGetSymbolAddress(scratch)");
-        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+        slot.ptr = static_cast<float*>(ptr);
     }
-    *out = g_scratch_ptr[dev];
-    return GEFEN_OK;
+    return slot.order.init(dev);
 }
 
 int check_step_task(const gefen_step_task& t) {
@@ -538,13 +623,30 @@ int check_codebook(const float* cb, int K) {
     return GEFEN_OK;
 }
 
+// gefen_step_tasks: check and plan every row, then run them with the pooled
+// stepsize tables.
+int step_tasks_general(const gefen_step_task* tasks, int ntasks, const CodebookTables* tables, hipStream_t st) {
+    std::vector<PendingStep> pend;
+    pend.reserve(ntasks);
+    for (int i = 0; i < ntasks; ++i) {
+        int rc = check_step_task(tasks[i]);
+        if (rc) return rc;
+        if (tasks[i].numel == 0) continue;
+        PendingStep ps;
+        rc = make_step_task(tasks[i], kVmeanUpdate, nullptr, ps);
+        if (rc) return rc;
+        pend.push_back(ps);
+    }
+    return run_steps_pooled(pend, tables, st);
+}
+
 // Temporary codebook tables for the single-call entry points.
 struct TempTables {
     void* ptr = nullptr;
     hipStream_t st = nullptr;
     int init(const float* cb, int K, hipStream_t s) {
         st = s;
-        hipError_t e = hipMallocAsync(&ptr, sizeof(CodebookTables), s);
+        hipError_t e = device_malloc_async(&ptr, sizeof(CodebookTables), s);
         if (e != hipSuccess) return hip_status(e, "hipMallocAsync(codebook tables)");
         return gefen_prepare_codebook(cb, K, ptr, reinterpret_cast<gefen_stream_t>(s));
     }
@@ -562,18 +664,8 @@ extern "C" int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const 
                                 gefen_stream_t stream) {
     if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
     if (!tables) return fail_inval("null codebook tables");
-    std::vector<PendingStep> pend;
-    pend.reserve(ntasks);
-    for (int i = 0; i < ntasks; ++i) {
-        int rc = check_step_task(tasks[i]);
-        if (rc) return rc;
-        if (tasks[i].numel == 0) continue;
-        PendingStep ps;
-        rc = make_step_task(tasks[i], kVmeanUpdate, nullptr, ps);
-        if (rc) return rc;
-        pend.push_back(ps);
-    }
-    return run_steps_pooled(pend, static_cast<const CodebookTables*>(tables), reinterpret_cast<hipStream_t>(stream));
+    return step_tasks_general(tasks, ntasks, static_cast<const CodebookTables*>(tables),
+                              reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int gefen_step_tasks_noalloc(const gefen_step_task* tasks, int ntasks, const void* tables,
@@ -599,17 +691,217 @@ extern "C" int gefen_step_tasks_noalloc(const gefen_step_task* tasks, int ntasks
                           "(at most %zu f16-state or %zu bf16-state (sqrt(bc2), eps, 1/bc1) settings per call)",
                           lp.total * sizeof(float), kNoAllocScratchFloats * sizeof(float), kNoAllocScratchFloats / kLutSlot,
                           kNoAllocScratchFloats / kRootSlot);
-    if (!lp.keys.empty()) {
-        int dev = 0;
-        int rc = stream_device(st, &dev);
-        if (rc) return rc;
-        float* base = nullptr;
-        rc = scratch_for_device(dev, &base);
-        if (rc) return rc;
-        rc = build_luts(pend, lp, base, st);
+    if (lp.keys.empty()) return flush_steps(pend, static_cast<const CodebookTables*>(tables), st, false);
+    int dev = 0;
+    int rc = stream_device(st, &dev);
+    if (rc) return rc;
+    ScratchSlot& slot = g_scratch[dev];
+    std::lock_guard<std::mutex> lock(slot.m);
+    rc = scratch_init(slot, dev);
+    if (rc) return rc;
+    // a call on another stream waits until the previous call's launches, which
+    // read the tables, are done (not under graph capture: there the graph orders them)
+    const bool cap = capturing(st);
+    if (!cap) {
+        rc = slot.order.wait(st);
         if (rc) return rc;
     }
-    return flush_steps(pend, static_cast<const CodebookTables*>(tables), st, false);
+    rc = build_luts(pend, lp, slot.ptr, st);
+    if (rc == GEFEN_OK) rc = flush_steps(pend, static_cast<const CodebookTables*>(tables), st, false);
+    return cap ? rc : slot.order.record(st, rc);
+}
+
+// ------------------------------------------------------------------------- step plan
+// gefen_step_plan: the launches of one task table, kept between steps.  At
+// creation the tasks are checked, their kernels chosen and grouped into
+// launches exactly as gefen_step_tasks does; a run checks that each row still
+// describes the same tensors (parameter and state pointers, sizes, period,
+// dtypes, and a gradient aligned for the chosen kernel), writes the per-step
+// values (gradient address and the scalars of set_step_scalars) into the kept
+// launch tables, rebuilds the period-one stepsize tables and launches.  A run
+// whose rows or stream do not fit the plan takes the gefen_step_tasks path.
+struct gefen_step_plan {
+    int dev = 0;
+    const CodebookTables* tables = nullptr;
+    int ntasks = 0;
+    std::vector<gefen_step_task> shape;  // the creation rows
+    std::vector<int> row;                // caller row of each pending task
+    std::vector<int> galign;             // gradient alignment (bytes) each pending task's kernel needs
+    std::vector<PendingStep> pend;
+    std::vector<StepLaunch> launches;
+    std::vector<int> slot;               // launch * kMaxBatch + position of each pending task
+    LutPlan lp;                          // stepsize tables of the current run
+    SideStream* side = nullptr;
+    bool timing = false, timed = false;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+
+namespace gefen {
+namespace {
+
+// The fields of a row that fix its kernel and launch slot.
+bool same_tensors(const gefen_step_task& a, const gefen_step_task& b) {
+    return a.p == b.p && a.m_codebook == b.m_codebook && a.m_magnitude == b.m_magnitude && a.vmean == b.vmean &&
+           a.numel == b.numel && a.period == b.period &&
+           (a.period != 1 || a.period_one_divisor == b.period_one_divisor) && a.param_dtype == b.param_dtype &&
+           a.state_dtype == b.state_dtype;
+}
+
+// The plan's fast path: a GEFEN_* status, or -1 when the rows do not fit the
+// plan (then nothing was launched).
+int plan_run_fast(gefen_step_plan& P, const gefen_step_task* tasks, hipStream_t st) {
+    for (size_t i = 0; i < P.pend.size(); ++i) {
+        const gefen_step_task& in = tasks[P.row[i]];
+        if (!same_tensors(in, P.shape[P.row[i]]) || !in.grad || !aligned(in.grad, P.galign[i])) return -1;
+        int rc = check_step_task(in);
+        if (rc) return rc;
+        StepTask& t = P.pend[i].task;
+        t.g = in.grad;
+        set_step_scalars(in, t);
+        t.lut = nullptr;
+    }
+    // every row that must be stepped as a no-op (numel 0) is still empty
+    for (int r = 0; r < P.ntasks; ++r)
+        if (tasks[r].numel != P.shape[r].numel) return -1;
+    plan_luts(P.pend, P.lp);
+    // one stepsize table per launch, as the grouping assumed
+    {
+        std::vector<int> key_of_launch(P.launches.size(), -2);
+        for (size_t i = 0; i < P.pend.size(); ++i) {
+            int& k = key_of_launch[(size_t)(P.slot[i] / kMaxBatch)];
+            if (k == -2) k = P.lp.which[i];
+            else if (k != P.lp.which[i]) return -1;
+        }
+    }
+    const bool timing = P.timing;
+    if (timing && hipEventRecord(P.t0, st) != hipSuccess) return launch_status("hipEventRecord(step plan)");
+    int rc = GEFEN_OK;
+    LutPool* pool = nullptr;
+    std::unique_lock<std::mutex> lock;
+    if (!P.lp.keys.empty()) {
+        pool = &g_lut_pool[P.dev];
+        lock = std::unique_lock<std::mutex>(pool->m);
+        rc = lut_pool_reserve(*pool, P.dev, P.lp.total, st);
+        if (rc) return rc;
+        rc = build_luts(P.pend, P.lp, pool->buf, st);
+    }
+    if (rc == GEFEN_OK) {
+        for (size_t i = 0; i < P.pend.size(); ++i) {
+            const int q = P.slot[i];
+            P.launches[(size_t)(q / kMaxBatch)].b.t[q % kMaxBatch] = P.pend[i].task;
+        }
+        rc = issue_launches(P.launches, st, true, P.side);
+    }
+    if (pool) rc = pool->order.record(st, rc);
+    if (timing) {
+        hipError_t e = hipEventRecord(P.t1, st);
+        if (e != hipSuccess && rc == GEFEN_OK) rc = hip_status(e, "hipEventRecord(step plan)");
+        P.timed = e == hipSuccess;
+    }
+    return rc;
+}
+
+}  // namespace
+}  // namespace gefen
+
+extern "C" int gefen_step_plan_create(const gefen_step_task* tasks, int ntasks, const void* tables,
+                                      gefen_step_plan** out) {
+    if (!out) return fail_inval("null plan pointer");
+    *out = nullptr;
+    if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
+    if (!tables) return fail_inval("null codebook tables");
+    int dev = 0;
+    int rc = stream_device(nullptr, &dev);
+    if (rc) return rc;
+    gefen_step_plan* P = new (std::nothrow) gefen_step_plan();
+    if (!P) return fail_inval("out of host memory");
+    P->dev = dev;
+    P->tables = static_cast<const CodebookTables*>(tables);
+    P->ntasks = ntasks;
+    P->shape.assign(tasks, tasks + ntasks);
+    for (int i = 0; i < ntasks; ++i) {
+        rc = check_step_task(tasks[i]);
+        if (rc == GEFEN_OK && tasks[i].numel > 0) {
+            PendingStep ps;
+            rc = make_step_task(tasks[i], kVmeanUpdate, nullptr, ps);
+            if (rc == GEFEN_OK) {
+                P->pend.push_back(ps);
+                P->row.push_back(i);
+                P->galign.push_back((ps.key.R == 0 ? 1 : ps.key.W) * dtype_size(ps.key.d));
+            }
+        }
+        if (rc) {
+            delete P;
+            return rc;
+        }
+    }
+    // group as gefen_step_tasks would, with the creation rows' stepsize-table keys
+    plan_luts(P->pend, P->lp);
+    for (size_t i = 0; i < P->pend.size(); ++i)
+        P->pend[i].task.lut = P->lp.which[i] >= 0 ? reinterpret_cast<const float*>((uintptr_t)(P->lp.which[i] + 1) * 256)
+                                                  : nullptr;
+    group_launches(P->pend, P->tables, P->launches, &P->slot);
+    for (PendingStep& ps : P->pend) ps.task.lut = nullptr;
+    P->side = side_stream_of(dev);
+    *out = P;
+    return GEFEN_OK;
+}
+
+extern "C" int gefen_step_plan_run(gefen_step_plan* plan, const gefen_step_task* tasks, int ntasks,
+                                   gefen_stream_t stream) {
+    if (!plan) return fail_inval("null step plan");
+    if (ntasks < 0 || (ntasks > 0 && !tasks)) return fail_inval("invalid task array");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    int dev = -1;
+    int rc = stream_device(st, &dev);
+    if (rc) return rc;
+    if (ntasks == plan->ntasks && dev == plan->dev) {
+        DeviceScope scope(dev);
+        rc = plan_run_fast(*plan, tasks, st);
+        if (rc != -1) return rc;
+    }
+    DeviceScope scope(dev);
+    const bool timing = plan->timing && dev == plan->dev;
+    if (timing && hipEventRecord(plan->t0, st) != hipSuccess) return launch_status("hipEventRecord(step plan)");
+    rc = step_tasks_general(tasks, ntasks, plan->tables, st);
+    if (timing) {
+        hipError_t e = hipEventRecord(plan->t1, st);
+        if (e != hipSuccess && rc == GEFEN_OK) rc = hip_status(e, "hipEventRecord(step plan)");
+        plan->timed = e == hipSuccess;
+    }
+    return rc;
+}
+
+extern "C" int gefen_step_plan_time_runs(gefen_step_plan* plan, int enable) {
+    if (!plan) return fail_inval("null step plan");
+    if (enable && !plan->t0) {
+        DeviceScope scope(plan->dev);
+        hipError_t e = hipEventCreate(&plan->t0);
+        if (e == hipSuccess) e = hipEventCreate(&plan->t1);
+        if (e != hipSuccess) return hip_status(e, "hipEventCreate(step plan)");
+    }
+    plan->timing = enable != 0;
+    plan->timed = false;
+    return GEFEN_OK;
+}
+
+extern "C" int gefen_step_plan_last_ms(gefen_step_plan* plan, float* ms) {
+    if (!plan || !ms) return fail_inval("null step plan or result pointer");
+    if (!plan->timed) return fail_inval("no timed run: enable gefen_step_plan_time_runs before a run");
+    hipError_t e = hipEventSynchronize(plan->t1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, plan->t0, plan->t1);
+    return hip_status(e, "hipEventElapsedTime(step plan)");
+}
+
+extern "C" void gefen_step_plan_destroy(gefen_step_plan* plan) {
+    if (!plan) return;
+    if (plan->t0 || plan->t1) {
+        DeviceScope scope(plan->dev);
+        if (plan->t1) (void)hipEventSynchronize(plan->t1);
+        if (plan->t0) (void)hipEventDestroy(plan->t0);
+        if (plan->t1) (void)hipEventDestroy(plan->t1);
+    }
+    delete plan;
 }
 
 static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_sign, void* mag,

@@ -19,6 +19,7 @@ device.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from itertools import chain
 from pathlib import Path
@@ -283,9 +284,10 @@ class _StepPlan:
 
     __slots__ = ("params", "pptr", "numel", "gdtype", "states", "state_keys", "srefs", "groups", "tasks", "device",
                  "dev_index",
-                 "grads", "gptr", "distinct", "group_index", "hyper", "core", "steps", "columns")
+                 "grads", "gptr", "distinct", "group_index", "hyper", "core", "steps", "columns", "tables", "handle",
+                 "lib")
 
-    def __init__(self, opt, items, tasks, device):
+    def __init__(self, opt, items, tasks, device, tables):
         self.params = [it[1] for it in items]
         self.pptr = [it[1].data_ptr() for it in items]
         self.numel = [it[3].numel() for it in items]
@@ -309,6 +311,32 @@ class _StepPlan:
         fields = self.tasks.dtype.fields
         self.columns = tuple(fields[c][1] for c in ("grad", "lr", "beta1", "beta2", "eps", "weight_decay",
                                                      "bias_correction_1", "bias_correction_2"))
+        # the launches of this table, kept by the library (gefen_step_plan): a step
+        # only rewrites gradient addresses and scalars before launching
+        self.lib = _lib.load()
+        self.tables = tables
+        self.handle = None
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            _lib.check(self.lib.gefen_step_plan_create(self.tasks.ctypes.data, len(self.tasks), tables.data_ptr(),
+                                                       ctypes.byref(handle)), "gefen_step_plan_create")
+        self.handle = handle.value
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            self.lib.gefen_step_plan_destroy(self.handle)
+            self.handle = None
+
+    def run(self, tasks, tables, stream) -> None:
+        """Steps the refreshed table on `stream` (the plan's device current):
+        through the kept launches, or with gefen_step_tasks when the codebook
+        tables are no longer the plan's."""
+        if tables is self.tables:
+            _lib.check(self.lib.gefen_step_plan_run(self.handle, tasks.ctypes.data, len(tasks), stream),
+                       "gefen_step_plan_run")
+        else:
+            _lib.check(self.lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), tables.data_ptr(), stream),
+                       "gefen_step_tasks")
 
     def refresh(self, opt):
         t = self.tasks
@@ -319,19 +347,20 @@ class _StepPlan:
                                      self.steps.ctypes.data):
                 return None
             return t
-        if _tensor_lr_with_decay(self.distinct):
-            return None
-        steps = _plan_checks_python(self, opt)
-        if steps is None:
-            return None
-        t["grad"] = self.gptr
         # hyperparameters once per distinct group (the table's columns are rewritten
         # only when they change), bias corrections once per (group, step)
         hyper = []
         for grp in self.distinct:
             glr = grp["lr"]
+            wd = _kernel_weight_decay(glr, grp["weight_decay"])
+            if wd is None:
+                return None
             hyper.append((float(glr.item()) if torch.is_tensor(glr) else float(glr), grp["beta1"], grp["beta2"],
-                          grp["eps"], grp["weight_decay"]))
+                          grp["eps"], wd))
+        steps = _plan_checks_python(self, opt)
+        if steps is None:
+            return None
+        t["grad"] = self.gptr
         t = self.tasks
         if hyper != self.hyper:
             gi = self.group_index
@@ -403,16 +432,25 @@ def _plan_checks_python(plan, opt):
     return steps
 
 
-def _decay_from_lr_tensor(lr, weight_decay) -> bool:
-    """Weight decay with a tensor lr whose dtype is not float64: torch forms the
-    factor 1 - lr * wd in that dtype (fl32(1 - fl32(lr * fl32(wd))) for float32),
-    not in double as the kernels do, so torch applies it before the launch."""
-    return weight_decay > 0.0 and torch.is_tensor(lr) and lr.dtype != torch.float64
-
-
-def _tensor_lr_with_decay(groups) -> bool:
-    """A group whose decay factor torch forms (no cached plan applies then)."""
-    return any(_decay_from_lr_tensor(g["lr"], g["weight_decay"]) for g in groups)
+def _kernel_weight_decay(lr, weight_decay):
+    """The weight decay to hand the kernels for a group (gefen.py:1280-1281,
+    p.mul_(1 - lr * wd)).  The kernels form the factor as (float)(1 - lr * wd) in
+    double.  For a float32 tensor lr torch forms it in float32,
+    f = fl32(1 - fl32(lr * fl32(wd))), which differs from the double expression in
+    about 1% of cases; the kernels then get wd' = (1 - f) / lr, for which the double
+    expression lies within ~2^-51 (relative) of f, far inside half a float ulp, so
+    it rounds to f exactly.  Returns wd' (wd itself for a number or float64 lr),
+    or None where that cannot hold (a tensor lr of a 16-bit dtype, lr <= 0, f zero
+    or not finite): torch then applies the factor before the launch."""
+    if not (weight_decay > 0.0 and torch.is_tensor(lr) and lr.dtype != torch.float64):
+        return weight_decay
+    if lr.dtype != torch.float32:
+        return None
+    lr_v = float(lr.item())
+    f = np.float32(np.float32(1.0) - np.float32(np.float32(lr_v) * np.float32(weight_decay)))
+    if not (lr_v > 0.0 and np.isfinite(f) and f != 0.0):
+        return None
+    return (1.0 - float(f)) / lr_v
 
 
 def _distinct(objs):
@@ -808,15 +846,12 @@ class Gefen(torch.optim.Optimizer):
             self._plan = None
             self._step_all_build()
             return
-        lib = _lib.load()
-        tables = self._codebook_tables().data_ptr()
+        tables = self._codebook_tables()
         if torch.cuda.current_device() == plan.dev_index:
-            rc = lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), tables, torch.cuda.current_stream().cuda_stream)
+            plan.run(tasks, tables, torch.cuda.current_stream().cuda_stream)
         else:
             with torch.cuda.device(plan.device):
-                rc = lib.gefen_step_tasks(tasks.ctypes.data, len(tasks), tables,
-                                          torch.cuda.current_stream(plan.device).cuda_stream)
-        _lib.check(rc, "gefen_step_tasks")
+                plan.run(tasks, tables, torch.cuda.current_stream(plan.device).cuda_stream)
 
     def _step_all_build(self) -> None:
         """_step_all from scratch: resolves every tensor, fills the task table and,
@@ -858,12 +893,11 @@ class Gefen(torch.optim.Optimizer):
                 raise ValueError("Expected grad_view dtype {} to match p dtype {}.".format(flat_grad.dtype,
                                                                                            fused_p.dtype))
             keep.append(flat_grad)
-            wd = group["weight_decay"]
-            if _decay_from_lr_tensor(lr_group, wd):
-                # p.mul_(1 - lr * wd) as gefen.py:1280-1281 evaluates it for a tensor lr
-                # (a double formula misses fl32(1 - fl32(lr * wd)) in ~1% of cases);
-                # the kernel then skips its own decay
-                fused_p.mul_(1 - lr_group * wd)
+            wd = _kernel_weight_decay(lr_group, group["weight_decay"])
+            if wd is None:
+                # p.mul_(1 - lr * wd) as gefen.py:1280-1281 evaluates it for a 16-bit
+                # tensor lr; the kernel then skips its own decay
+                fused_p.mul_(1 - lr_group * group["weight_decay"])
                 wd = 0.0
             t = tasks[i]
             t["p"] = fused_p.data_ptr()
@@ -894,7 +928,7 @@ class Gefen(torch.optim.Optimizer):
             local_p.copy_(fused_p)
         del keep
         if plain and all(it[3].device == dev for it in items):
-            self._plan = _StepPlan(self, items, tasks, dev)
+            self._plan = _StepPlan(self, items, tasks, dev, tables)
 
     def _optimizer_state_memory_bytes(self) -> int:
         return sum(v.numel() * v.element_size() for s in self.state.values() for v in s.values() if torch.is_tensor(v))

@@ -19,7 +19,7 @@ import torch.nn as nn
 
 from gefen_amd import _lib
 from gefen_amd.gefen import (Gefen, _DTYPE_CODE, _distinct, _gefen_host, _plan_checks_python,
-                             _decay_from_lr_tensor, _tensor_lr_with_decay, automatic_partition_view)
+                             _kernel_weight_decay, automatic_partition_view)
 
 EPS = 1e-7
 _SUMSQ_STRIDE = 128  # GEFEN_SUMSQ_STRIDE (include/gefen_hip.h): sum-of-squares entries per momentum task
@@ -256,11 +256,11 @@ class GefenMuon(Gefen):
                 raise ValueError("GefenMuon fused update requires a contiguous parameter tensor for {}.".format(
                     group["name"]))
             keep.append(target)
-            wd = group["weight_decay"]
-            if _decay_from_lr_tensor(lr_group, wd):
-                # p.mul_(1 - lr * wd) with a tensor lr (gefen_muon.py:325-326): the factor
-                # in the tensor's dtype, as torch forms it; the apply kernel skips its decay
-                target.mul_(1 - lr_group * wd)
+            wd = _kernel_weight_decay(lr_group, group["weight_decay"])
+            if wd is None:
+                # p.mul_(1 - lr * wd) with a 16-bit tensor lr (gefen_muon.py:325-326): the
+                # factor in the tensor's dtype, as torch forms it; the apply kernel skips its decay
+                target.mul_(1 - lr_group * group["weight_decay"])
                 wd = 0.0
             t = apply[i]
             t["p"] = target.data_ptr()
@@ -354,16 +354,14 @@ class _MuonPlan:
         out = []
         for g in self.distinct:
             lr = g["lr"]
-            out.append(((float(lr.item()) if torch.is_tensor(lr) else float(lr), g["weight_decay"], g["momentum"],
-                         bool(g["nesterov"])),
+            out.append(((float(lr.item()) if torch.is_tensor(lr) else float(lr),
+                         _kernel_weight_decay(lr, g["weight_decay"]), g["momentum"], bool(g["nesterov"])),
                         (tuple(g["ns_coefficients"]), g["ns_steps"], g["eps"], g["adjust_lr_fn"])))
         return out
 
     def refresh(self, opt) -> bool:
-        if _tensor_lr_with_decay(self.distinct):
-            return False
         settings = self._settings()
-        if any(a[1] != b[1] for a, b in zip(settings, self.settings)):
+        if any(a[1] != b[1] or a[0][1] is None for a, b in zip(settings, self.settings)):
             return False
         if self.core is not None:
             if not self.core.refresh(opt.param_groups, self.mtasks.ctypes.data, self.mtasks.itemsize, self.mcols,

@@ -34,6 +34,10 @@ enum { GEFEN_F32 = 0, GEFEN_F16 = 1, GEFEN_BF16 = 2 };
 
 const char* gefen_last_error(void);
 int gefen_abi_version(void);
+/* Number of device-memory allocations the library has made since it was loaded
+ * (its pools, workspaces and temporaries; never the caller's tensors).  A
+ * diagnostic: gefen_step_tasks_noalloc leaves it unchanged. */
+int64_t gefen_device_allocations(void);
 /* sizeof(gefen_step_task) for which = 0, sizeof(gefen_muon_task) for which = 1,
  * sizeof(gefen_muon_apply_task) for which = 2:
  * lets bindings check their mirror of the structs. */
@@ -140,10 +144,41 @@ int gefen_step_tasks(const gefen_step_task* tasks, int ntasks, const void* table
  * distinct f16-state or 682 distinct bf16-state (sqrt(bias_correction_2), eps,
  * 1/bias_correction_1) settings per call, else GEFEN_EINVAL before anything is
  * launched.  Every launch runs on `stream` (no side stream).  Calls on one
- * device share that buffer, which keeps the last call's tables: calls that
- * overlap on one device (other streams, other threads) race. */
+ * device share that buffer, which keeps the last call's tables: a call on
+ * another stream than the previous call that wrote the tables waits for that
+ * call's launches (an event per device, created on first use), and calls from
+ * several threads are serialised.  Under graph capture no such wait is
+ * recorded: a captured call and calls outside the graph that overlap with its
+ * replays on one device race. */
 int gefen_step_tasks_noalloc(const gefen_step_task* tasks, int ntasks, const void* tables,
                              gefen_stream_t stream);
+
+/* A prepared step: gefen_step_tasks for a task table whose tensors stay the
+ * same from step to step (the optimizer's cached plan).  No single counterpart
+ * in the reference: it replaces the per-parameter loop of Gefen.step
+ * (gefen.py:1409-1415) and its one or two launches per tensor, like
+ * gefen_step_tasks, and keeps what gefen_step_tasks redoes on every call: the
+ * row checks, kernel choices, grouping into launches and the launch tables.
+ *
+ * gefen_step_plan_create: tasks as for gefen_step_tasks (checked the same way);
+ * `tables` is kept by pointer; the plan belongs to the current device.
+ * gefen_step_plan_run: steps `tasks` (ntasks rows) exactly as gefen_step_tasks
+ * would.  Only the gradient address and the scalars (betas, lr, eps, weight
+ * decay, bias corrections) of a row may change cheaply; a table whose rows name
+ * other tensors (parameter or state pointers, sizes, period, dtypes), whose
+ * gradients lose the alignment their kernels were chosen for, or a stream of
+ * another device takes the gefen_step_tasks path.  One plan must not be run
+ * from two threads at once.
+ * gefen_step_plan_time_runs: enable != 0 makes each later run record two
+ * timing events on its stream, right before its first launch and after its
+ * last; gefen_step_plan_last_ms waits for the last timed run to finish and
+ * gives the GPU time between them in milliseconds. */
+typedef struct gefen_step_plan gefen_step_plan;
+int gefen_step_plan_create(const gefen_step_task* tasks, int ntasks, const void* tables, gefen_step_plan** plan);
+int gefen_step_plan_run(gefen_step_plan* plan, const gefen_step_task* tasks, int ntasks, gefen_stream_t stream);
+int gefen_step_plan_time_runs(gefen_step_plan* plan, int enable);
+int gefen_step_plan_last_ms(gefen_step_plan* plan, float* ms);
+void gefen_step_plan_destroy(gefen_step_plan* plan);
 
 /* GefenMuon momentum of many tensors with the Nesterov blend fused
  * (gefen_muon.py:302-316): out = D(D(q*mu) + g*(1-mu)) if nesterov, else q. */

@@ -226,8 +226,51 @@ def test_plan_core_checks_and_commits_only_when_the_plan_applies():
     unchanged_after(lambda: states[2].__setitem__("vmean", vm.clone()), lambda: states[2].__setitem__("vmean", vm))
     unchanged_after(lambda: states[0].__setitem__("step", torch.tensor(5)), lambda: states[0].__setitem__("step", 9))
     unchanged_after(lambda: groups[1].__setitem__("lr", "fast"), lambda: groups[1].__setitem__("lr", 2e-3))
-    # a float32 lr tensor with weight decay: torch forms that decay factor (no plan)
-    unchanged_after(lambda: groups[1].__setitem__("lr", torch.tensor(2e-3, dtype=torch.float32)),
+    # a bf16 lr tensor with weight decay: torch forms that decay factor in bf16 (no plan)
+    unchanged_after(lambda: groups[1].__setitem__("lr", torch.tensor(2e-3, dtype=torch.bfloat16)),
                     lambda: groups[1].__setitem__("lr", 2e-3))
     assert [st["step"] for st in states] == [12, 13, 13] and steps.tolist() == [12, 13, 13]
     assert table["bias_correction_1"].tolist() == [1 - 0.9 ** 12, 1 - 0.9 ** 13, 1 - 0.8 ** 13]
+    # a float32 lr tensor with weight decay keeps the plan: the row carries the
+    # weight decay for which the kernels' double factor is torch's float32 one
+    from gefen_amd.gefen import _kernel_weight_decay
+
+    lr32 = torch.tensor(2e-3, dtype=torch.float32)
+    groups[1]["lr"] = lr32
+    assert refresh(groups)
+    assert table["lr"][2] == float(lr32.item())
+    assert table["weight_decay"][2] == _kernel_weight_decay(lr32, 0.1) != 0.1
+    assert np.float32(1.0 - table["lr"][2] * table["weight_decay"][2]) == (1 - lr32 * 0.1).item()
+
+
+def test_kernel_weight_decay_reproduces_torch_float32_factor():
+    """_kernel_weight_decay: for a float32 tensor lr, the kernels' double expression
+    (float)(1 - lr * wd') equals torch's float32 factor 1 - lr * wd for every
+    sampled pair (including ones where the double expression with wd itself does
+    not), and decays exactly when that factor is below one; a 16-bit lr, a zero
+    factor or lr <= 0 are left to torch (None)."""
+    import numpy as np
+    import torch
+
+    from gefen_amd.gefen import _kernel_weight_decay
+
+    rng = np.random.default_rng(17)
+    lrs = np.concatenate([10.0 ** rng.uniform(-8, 0.5, 20000), [1e-3, 0.5, 1.0, 2.0, 3e-45, 1e-30]])
+    wds = np.concatenate([10.0 ** rng.uniform(-6, 1, 20000), [0.1, 2.0, 1.0, 0.5, 1e-3, 1e-9]])
+    differs = 0
+    for lr_v, wd in zip(lrs, wds):
+        lr = torch.tensor(float(lr_v), dtype=torch.float32)
+        torch_f = (1 - lr * float(wd)).item()
+        w = _kernel_weight_decay(lr, float(wd))
+        if torch_f == 0.0 or not lr.item() > 0.0:
+            assert w is None
+            continue
+        kernel_f = np.float32(1.0 - float(lr.item()) * w)
+        assert kernel_f == np.float32(torch_f), (lr_v, wd)
+        assert (w > 0.0) == (torch_f < 1.0)
+        differs += np.float32(1.0 - float(lr.item()) * float(wd)) != np.float32(torch_f)
+    assert differs > 100
+    assert _kernel_weight_decay(torch.tensor(1e-3, dtype=torch.bfloat16), 0.1) is None
+    assert _kernel_weight_decay(torch.tensor(0.5, dtype=torch.float32), 2.0) is None  # factor 0
+    assert _kernel_weight_decay(torch.tensor(1e-3, dtype=torch.float64), 0.1) == 0.1
+    assert _kernel_weight_decay(1e-3, 0.1) == 0.1 and _kernel_weight_decay(torch.tensor(1e-3), 0.0) == 0.0

@@ -2,8 +2,9 @@
 gefen_muon.py:325-326: p.mul_(1 - lr * wd)): torch forms the decay factor in the
 tensor's dtype, fl32(1 - fl32(lr * fl32(wd))) for a float32 lr, which differs
 from the double expression (float)(1 - lr * wd) in about 1% of cases.  The
-optimizer applies that factor as torch does; the rest of the step is the
-ordinary one."""
+optimizer hands the kernels the weight decay for which their factor is torch's
+(gefen._kernel_weight_decay), so such steps keep the cached plan; the rest of
+the step is the ordinary one."""
 
 import numpy as np
 import pytest
@@ -62,6 +63,7 @@ def test_gefen_tensor_lr_weight_decay_matches_oracle(dtype):
     opt._gefen_codebook = torch.from_numpy(cb).to("cuda:0")
     ref = orc.GefenOracle(arrs, codebook=cb)
     fac = torch_decay_factor(lr, wd)
+    planned = 0
     for step in range(1, 4):
         grads = []
         for i, (t, shape) in enumerate(zip(tensors, shapes)):
@@ -69,6 +71,7 @@ def test_gefen_tensor_lr_weight_decay_matches_oracle(dtype):
             g = syn.round_to(syn.row_scaled_normal(21, 100 * step + i, rows, t.numel() // rows, -14, -4), dtype)
             grads.append(g.reshape(-1))
             t.grad = gu.to_dev(g.reshape(-1), dtype).reshape(shape)
+        planned += opt._plan is not None
         opt.step()
         # the oracle step with the decay applied first with torch's factor
         for prm in arrs:
@@ -82,3 +85,4 @@ def test_gefen_tensor_lr_weight_decay_matches_oracle(dtype):
             assert tu.ulp_distance_bf16(got, arrs[i]["p"]).max() <= 1
         else:
             np.testing.assert_allclose(got, arrs[i]["p"], rtol=1e-5, atol=1e-7)
+    assert planned == 2  # the tensor lr with weight decay keeps the cached plan from the second step on

@@ -1,8 +1,9 @@
 """gefen_step_tasks_noalloc (the step entry point that allocates nothing) against
 gefen_step_tasks, through the C ABI: bit-identical parameters, indices,
 magnitudes and vmean on two calls in a row, the second with smaller tensors;
-and the host-side rejection of a call whose stepsize tables exceed the scratch
-buffer."""
+the host-side rejection of a call whose stepsize tables exceed the scratch
+buffer; the library's device-allocation count unchanged by it in a fresh
+process; and two calls on two streams ordered by the scratch buffer's event."""
 
 import numpy as np
 import pytest
@@ -106,3 +107,82 @@ def test_noalloc_rejects_tables_beyond_its_scratch_buffer():
     assert b"scratch buffer" in lib.gefen_last_error()
     _lib.check(lib.gefen_step_tasks(t.ctypes.data, len(specs), tables.data_ptr(), gu.stream()))
     torch.cuda.synchronize()
+
+
+_CHILD = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import torch
+import test_zz_no_alloc as t
+from gefen_amd import _lib
+
+lib = _lib.load()
+tables = t._tables(lib)
+before = lib.gefen_device_allocations()
+specs = t._tensor_set(14, [("bf16", 1 << 16, 1), ("f16", 4096, 1), ("bf16", 8 * 2048, 2048)])
+ps = [t.gu.to_dev(s[4], s[0]) for s in specs]
+gs = [t.gu.to_dev(s[5], s[0]) for s in specs]
+states = [t._state(*s[:4]) for s in specs]
+for step in (1, 2):
+    tk = t._tasks(specs, ps, gs, states, step)
+    _lib.check(lib.gefen_step_tasks_noalloc(tk.ctypes.data, len(specs), tables.data_ptr(), t.gu.stream()))
+torch.cuda.synchronize()
+after_noalloc = lib.gefen_device_allocations()
+tk = t._tasks(specs, ps, gs, states, 3)
+_lib.check(lib.gefen_step_tasks(tk.ctypes.data, len(specs), tables.data_ptr(), t.gu.stream()))
+torch.cuda.synchronize()
+print("allocations", before, after_noalloc, lib.gefen_device_allocations(), flush=True)
+'''
+
+
+def test_noalloc_allocates_nothing():
+    """In a fresh process (no stepsize-table pool yet), two no-allocation calls with
+    period-one bf16 and f16 states leave the library's device-allocation count
+    unchanged, while gefen_step_tasks on the same tensors allocates its pool: the
+    count sees the allocation the no-allocation entry point avoids."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = str(Path(__file__).resolve().parent.parent)
+    r = subprocess.run([sys.executable, "-c", _CHILD, repo], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    line = [ln for ln in r.stdout.splitlines() if ln.startswith("allocations")][-1]
+    before, after_noalloc, after_step = map(int, line.split()[1:])
+    print(line, flush=True)
+    assert after_noalloc == before
+    assert after_step > after_noalloc
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """Two no-allocation calls on two streams, back to back, with different eps (so
+    the second call rewrites the stepsize tables in the shared scratch buffer while
+    the first call's launches may still read them): the second waits for the first,
+    and each equals gefen_step_tasks bit for bit."""
+    lib = _lib.load()
+    tables = _tables(lib)
+    shapes = [("bf16", 1 << 23, 1), ("f16", 1 << 20, 1)]
+    runs = {}
+    for entry in ("gefen_step_tasks", "gefen_step_tasks_noalloc"):
+        sets = []
+        for k, seed in enumerate((15, 16)):
+            specs = _tensor_set(seed, shapes)
+            ps = [gu.to_dev(s[4], s[0]) for s in specs]
+            gs = [gu.to_dev(s[5], s[0]) for s in specs]
+            states = [_state(*s[:4]) for s in specs]
+            sets.append((specs, ps, gs, states, _tasks(specs, ps, gs, states, 1, eps_of=lambda i, k=k: 1e-8 * (k + 1))))
+        torch.cuda.synchronize()
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for (specs, _, _, _, tk), s in zip(sets, streams):
+            _lib.check(getattr(lib, entry)(tk.ctypes.data, len(specs), tables.data_ptr(), s.cuda_stream), entry)
+        torch.cuda.synchronize()
+        runs[entry] = [([gu.to_np(p) for p in ps], [{k: gu.to_np(v) for k, v in st.items()} for st in states])
+                       for (_, ps, _, states, _) in sets]
+    for k in range(2):
+        for i in range(len(shapes)):
+            ref_p, ref_s = runs["gefen_step_tasks"][k]
+            got_p, got_s = runs["gefen_step_tasks_noalloc"][k]
+            np.testing.assert_array_equal(got_p[i], ref_p[i], err_msg="call {} p{}".format(k, i))
+            for key in ("idx", "mag", "vmean"):
+                np.testing.assert_array_equal(got_s[i][key], ref_s[i][key], err_msg="call {} {}{}".format(k, key, i))
