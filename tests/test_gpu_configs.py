@@ -7,17 +7,27 @@ copied from the device):
 * every tensor's automatic period equals oracle.find_period;
 * the learned codebook equals oracle.learn_codebook, bit for bit;
 * sampled tensors (the embedding, the last tensor, a block-row matrix, a
-  period-one matrix where the configuration has one, a norm or bias) over three
-  steps with a new gradient each step, each step checked on its own (the oracle
-  starts every step from the GPU's parameters and state): codebook indices and
-  magnitudes bit-exact, vmean within rtol 2^-18 (float32: the block mean of g^2
-  summed in another order) or 1 bf16 ulp, parameters within rtol 1e-5 /
-  atol 1e-7 (fp32) or 1 bf16 ulp.  A bf16 block mean of g^2 summed in another
-  order can round to the neighbouring bf16 value (the oracle sums in double, the
-  reference and the GPU in float32, each in its own order); that changes the
-  stepsize by at most 2^-8 relative, so a parameter whose update nearly cancels
-  it may differ by more than one ulp of the small result: such an element must
-  lie in a row whose vmean differs, and within 2^-7 of the update.
+  period-one matrix where the configuration has one, a norm or bias) over the
+  configuration's stated number of steps (GPT-2 and Llama-1.5B 20, Llama-8B 10),
+  a new gradient each step, with the oracle running on its own (never
+  resynchronised from the GPU): codebook indices and magnitudes bit-exact at
+  every step (the momentum state depends only on the gradients).  GPT-2 (fp32):
+  vmean within rtol 2^-16 and parameters within rtol 1e-5 / atol 1e-7 after 20
+  steps; GPT-2 also step by step over three steps with the oracle started from
+  the GPU's state each step.
+* bf16 configs: a block mean of g^2 summed in another order (the oracle sums in
+  double, the reference and the GPU in float32, each in its own order) can round
+  to the neighbouring bf16 vmean; from then on that row's stepsize differs by at
+  most ~2^-8 relative and its parameters drift apart by a small fraction of the
+  update.  Every other row (every period-one tensor: vmean is element-wise
+  there) must stay bit-exact.  Rows whose vmean has differed at some step are
+  tracked: their vmean within 2 ulps, their parameters within
+  2^-7 * (sum of the oracle's per-step |update|) + (steps) * ulp.  The count and
+  fraction of those rows and of the elements beyond one ulp are printed and
+  bounded: at most 1e-2 of a tensor's rows (a float32 sum of 2048 squares is
+  within ~2^-21 relative of the exact one, so a row's bf16 vmean flips with
+  probability ~2^-12 / k at step k, ~1e-3 over 20 steps) and 1e-3 of the
+  sampled elements.
 """
 
 import numpy as np
@@ -200,12 +210,97 @@ def test_gpt2_124m_fp32_twenty_free_running_steps_match_oracle():
                   float(np.max(err / (1e-7 + 1e-5 * np.abs(ref.params[k]["p"]))))), flush=True)
 
 
-def test_llama_1_5b_bf16_full_config_matches_oracle():
-    _run("llama1.5b")
+def _free_running_bf16(config, steps):
+    """config (bf16) at full size: periods and codebook against the oracle after the
+    first step, then `steps` steps with the oracle running on its own for the
+    sampled tensors (see the module docstring for the bars)."""
+    import bench
+    from gefen_amd.gefen import Gefen
+
+    print("config", config, "free running for", steps, "steps", flush=True)
+    cfg = bench.CONFIGS[config]
+    dev = torch.device("cuda:0")
+    params = bench.build_problem(cfg, dev)
+    grads = [_host(p.grad) for _, p in params]
+    opt = Gefen(params)
+    opt.step()
+    torch.cuda.synchronize()
+    periods = [opt.state[p]["automatic_period"] for _, p in params]
+    ref_periods = [1 if g.size == 1 else orc.find_period(g, "bf16") for g in grads]
+    bad = [(params[i][0], a, b) for i, (a, b) in enumerate(zip(periods, ref_periods)) if a != b]
+    assert not bad, bad
+    ref_cb = orc.learn_codebook([(g, "bf16", P) for g, P in zip(grads, ref_periods)])
+    np.testing.assert_array_equal(opt._gefen_codebook.detach().cpu().numpy(), ref_cb)
+    print("periods and codebook match the oracle", flush=True)
+    sample = _sample(params, opt)
+    kinds = {("one" if periods[i] == 1 else "rows") if params[i][1].dim() == 2 else "vector" for i in sample}
+    assert {"rows", "one", "vector"} <= kinds, sample
+    arrs = [{"p": _initial(cfg, params, i), "dtype": "bf16", "shape": tuple(params[i][1].shape), "lr": 1e-3,
+             "beta1": 0.9, "beta2": 0.999, "eps": 1e-8, "weight_decay": 0.0} for i in sample]
+    ref = orc.GefenOracle(arrs, codebook=ref_cb)
+    ref.periods = [ref_periods[i] for i in sample]
+    ref_g = [grads[i] for i in sample]
+    del grads
+    flagged = [None] * len(sample)  # per sampled tensor: rows whose vmean has differed
+    cum = [np.zeros(params[i][1].numel(), dtype=np.float32) for i in sample]  # the oracle's |update| sums there
+    beyond_total = elems_total = 0
+    for step in range(1, steps + 1):
+        if step > 1:
+            for i, (_, p) in enumerate(params):
+                bench.fill_grad(cfg, p.grad, i, step)
+            opt.step()
+            torch.cuda.synchronize()
+            ref_g = [_host(params[i][1].grad) for i in sample]
+        before = [a["p"].copy() for a in arrs]
+        ref.step(ref_g)
+        for k, i in enumerate(sample):
+            name, p = params[i]
+            st, rs = opt.state[p], ref.state[k]
+            tag = "{} {} step {}".format(config, name, step)
+            assert rs.step == st["step"] == step, tag
+            np.testing.assert_array_equal(_host(st["m_codebook"]), rs.m_codebook, err_msg=tag + " indices")
+            np.testing.assert_array_equal(_host(st["m_magnitude"]), rs.m_magnitude, err_msg=tag + " magnitudes")
+            got_v = _host(st["vmean"])
+            dv = tu.ulp_distance_bf16(got_v, rs.vmean)
+            assert dv.max() <= 2, tag + " vmean"
+            flag = flagged[k] = (dv > 0) if flagged[k] is None else (flagged[k] | (dv > 0))
+            ref_p = ref.params[k]["p"]
+            per_row = ref_p.size // got_v.size
+            # |update| of this step summed over the steps, in the flagged rows (elsewhere unused)
+            frows = np.nonzero(flag)[0]
+            if frows.size:
+                fe = (frows[:, None] * per_row + np.arange(per_row)[None, :]).reshape(-1)
+                cum[k][fe] += np.abs(orc.to_f32(ref_p[fe], "bf16") - orc.to_f32(before[k][fe], "bf16"))
+            got_p = _host(p)
+            off = np.nonzero(got_p != ref_p)[0]
+            # outside the flagged rows: bit-exact
+            outside = off[~flag[off // per_row]]
+            assert outside.size == 0, (tag, outside[:8])
+            d = tu.ulp_distance_bf16(got_p[off], ref_p[off])
+            diff = np.abs(orc.to_f32(got_p[off], "bf16").astype(np.float64) -
+                          orc.to_f32(ref_p[off], "bf16").astype(np.float64))
+            bound = 2.0 ** -7 * cum[k][off].astype(np.float64) + step * orc.ulp_bf16(ref_p[off])
+            assert np.all(diff <= bound), (tag, off[diff > bound][:8])
+            if step == steps:
+                nflag = int(frows.size)
+                beyond = int((d > 1).sum())
+                beyond_total += beyond
+                elems_total += ref_p.size
+                print("{}: period {}, {} of {} rows with a vmean that differed at some step, {} of {} elements "
+                      "differ ({} beyond one ulp)".format(tag, periods[i], nflag, flag.size, off.size, ref_p.size,
+                                                           beyond), flush=True)
+                assert nflag <= max(1, 1e-2 * flag.size), tag
+    print("{} after {} steps: {} of {} sampled elements beyond one bf16 ulp ({:.2e})".format(
+        config, steps, beyond_total, elems_total, beyond_total / elems_total), flush=True)
+    assert beyond_total <= 1e-3 * elems_total
 
 
-def test_llama_8b_bf16_full_config_matches_oracle():
-    _run("llama8b")
+def test_llama_1_5b_bf16_twenty_free_running_steps_match_oracle():
+    _free_running_bf16("llama1.5b", 20)
+
+
+def test_llama_8b_bf16_ten_free_running_steps_match_oracle():
+    _free_running_bf16("llama8b", 10)
 
 
 def test_full_size_period_scores_match_reference():

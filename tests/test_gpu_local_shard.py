@@ -8,8 +8,13 @@ on one GPU with tensor subclasses standing in for torch's distributed types:
   materialised gradients): the period scoring catches the error, materialises it
   with add_(0) and scores again.
 
-Every case must give the same parameters and state, bit for bit, as the same
-step on plain tensors."""
+The plain-tensor run is checked against the CPU oracle (GefenOracle /
+GefenMuonOracle on the same inputs: periods, learned codebook, codebook indices
+and magnitudes bit-exact; fp32 parameters within rtol 1e-5 / atol 1e-7, bf16
+within one ulp outside rows whose vmean rounded the other way; GefenMuon
+parameters within 5% of the update norm, the bound its Newton-Schulz products
+allow, tests/test_gpu_optimizer.py), and every wrapped case must give the same
+parameters and state as the plain run, bit for bit."""
 
 import numpy as np
 import pytest
@@ -94,6 +99,53 @@ def _run(opt_cls, dtype, wrap_param, wrap_grad, steps=3, **kw):
     return params, opt
 
 
+def _oracle_check(params, opt, dtype, steps=3, muon=False):
+    """The plain-tensor run (params, opt) against the CPU oracle on the same inputs."""
+    import gpu_util as gu
+    import traj_util as tu
+    from oracle import oracle as orc
+
+    dt = "bf16" if dtype == torch.bfloat16 else "f32"
+    p0 = [gu.to_np(t).reshape(-1) for t in _params(dtype)]
+    g0 = opt.param_groups[0]
+    if muon:
+        arrs = [{"p": p.copy(), "dtype": dt, "shape": s, "lr": g0["lr"], "beta1": g0["momentum"], "beta2": 0.0,
+                 "eps": g0["eps"], "weight_decay": g0["weight_decay"]} for p, s in zip(p0, SHAPES)]
+        ref = orc.GefenMuonOracle(arrs, momentum=g0["momentum"], nesterov=g0["nesterov"],
+                                  ns_coefficients=tuple(g0["ns_coefficients"]), ns_steps=g0["ns_steps"],
+                                  eps=g0["eps"], adjust_lr_fn=g0["adjust_lr_fn"])
+    else:
+        arrs = [{"p": p.copy(), "dtype": dt, "shape": s, "lr": g0["lr"], "beta1": g0["beta1"], "beta2": g0["beta2"],
+                 "eps": g0["eps"], "weight_decay": g0["weight_decay"]} for p, s in zip(p0, SHAPES)]
+        ref = orc.GefenOracle(arrs)
+    for step in range(steps):
+        ref.step([gu.to_np(g).reshape(-1) for g in _inputs(dtype, step)])
+    np.testing.assert_array_equal(opt._gefen_codebook.detach().cpu().numpy(), ref.codebook)
+    for i, (prm, t) in enumerate(zip(arrs, params)):
+        st = opt.state[t]
+        assert st["automatic_period"] == ref.periods[i], i
+        np.testing.assert_array_equal(gu.to_np(st["m_codebook"]).reshape(-1), ref.state[i].m_codebook)
+        np.testing.assert_array_equal(gu.to_np(st["m_magnitude"]).reshape(-1), ref.state[i].m_magnitude)
+        got = gu.to_np(t.to_local() if hasattr(t, "to_local") else t).reshape(-1)
+        if muon:
+            ours = orc.to_f32(got, dt).astype(np.float64) - orc.to_f32(p0[i], dt)
+            theirs = orc.to_f32(prm["p"], dt).astype(np.float64) - orc.to_f32(p0[i], dt)
+            rel = np.linalg.norm(ours - theirs) / max(np.linalg.norm(theirs), 1e-30)
+            print("local shard oracle: muon p{} relative update error {:.3g}".format(i, rel), flush=True)
+            assert rel <= 0.05, (i, rel)
+        elif dt == "f32":
+            np.testing.assert_allclose(got, prm["p"], rtol=1e-5, atol=1e-7)
+        else:
+            d = tu.ulp_distance_bf16(got, prm["p"])
+            far = np.nonzero(d > 1)[0]
+            if far.size:  # only in rows whose bf16 vmean rounded the other way
+                vm = gu.to_np(st["vmean"]).reshape(-1)
+                dv = tu.ulp_distance_bf16(vm, ref.state[i].vmean)
+                assert np.all(dv[far // (got.size // vm.size)] > 0), (i, far[:8])
+            print("local shard oracle: p{} period {}: {} of {} elements exact, {} beyond one ulp".format(
+                i, ref.periods[i], int((d == 0).sum()), d.size, far.size), flush=True)
+
+
 def _same(a_params, a_opt, b_params, b_opt):
     for pa, pb in zip(a_params, b_params):
         la = pa.to_local() if hasattr(pa, "to_local") else pa
@@ -112,15 +164,18 @@ def test_dtensor_like_parameters_and_gradients(dtype):
     from gefen_amd.gefen import Gefen
 
     base = _run(Gefen, dtype, lambda t: t, lambda g: g)
+    _oracle_check(*base, dtype)
     shard = _run(Gefen, dtype, lambda t: LocalShard(t), lambda g: LocalShard(g))
     assert all(type(p) is LocalShard for p in shard[0])
     _same(*base, *shard)
+    _oracle_check(*shard, dtype)
 
 
 def test_waitable_gradients():
     from gefen_amd.gefen import Gefen
 
     base = _run(Gefen, torch.bfloat16, lambda t: t, lambda g: g)
+    _oracle_check(*base, torch.bfloat16)
     waited = _run(Gefen, torch.bfloat16, lambda t: t, lambda g: Pending(g))
     _same(*base, *waited)
 
@@ -130,6 +185,7 @@ def test_lazily_materialised_gradient_is_added_zero_and_rescored():
 
     Lazy = make_lazy_class()
     base = _run(Gefen, torch.bfloat16, lambda t: t, lambda g: g, steps=1)
+    _oracle_check(*base, torch.bfloat16, steps=1)
     lazy = _run(Gefen, torch.bfloat16, lambda t: t, lambda g: Lazy(g), steps=1)
     assert Lazy.allocated and Lazy.touched_before_allocation == 1
     _same(*base, *lazy)
@@ -143,10 +199,11 @@ def test_gefen_muon_with_dtensor_like_parameters():
     SHAPES = [(64, 96), (128, 48)]  # GefenMuon: 2-D parameters only
     try:
         base = _run(GefenMuon, torch.bfloat16, lambda t: t, lambda g: g)
+        _oracle_check(*base, torch.bfloat16, muon=True)
         shard = _run(GefenMuon, torch.bfloat16, lambda t: LocalShard(t), lambda g: LocalShard(g))
+        _same(*base, *shard)
     finally:
         SHAPES = saved
-    _same(*base, *shard)
 
 
 def test_dequantised_momentum_keeps_the_dtensor_type():

@@ -92,8 +92,9 @@ def test_step_plan_runs_equal_step_tasks():
     steps = [1] * len(SPECS)
     grads = _grads(31, 1)
     plan = ctypes.c_void_p()
-    _lib.check(lib.gefen_step_plan_create(a.tasks(grads, steps).ctypes.data, len(SPECS), tables.data_ptr(),
-                                          ctypes.byref(plan)), "gefen_step_plan_create")
+    t0 = a.tasks(grads, steps)  # referenced until the call returns
+    _lib.check(lib.gefen_step_plan_create(t0.ctypes.data, len(SPECS), tables.data_ptr(), ctypes.byref(plan)),
+               "gefen_step_plan_create")
     try:
         _lib.check(lib.gefen_step_plan_time_runs(plan, 1))
         for step in range(1, 9):
