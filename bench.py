@@ -441,29 +441,42 @@ def cpu_baseline(opt, params, budget_s=20.0):
 
 
 def cpu_baseline_muon(opt, params, budget_s=20.0):
-    """Oracle GefenMuon step (quantised momentum and Nesterov blend in C, the
-    Newton-Schulz products in float64 numpy with a bf16 rounding per torch op,
-    the parameter update) on a sample of matrices, scaled by Newton-Schulz flops
-    to one full step: the CPU restatement of the reference's path
-    (gefen_muon.py:16-51, 132-171, 302-329)."""
+    """The GefenMuon step of the reference's CPU path on one matrix of each shape,
+    scaled by Newton-Schulz flops to one full step: quantised momentum and the
+    Nesterov blend from the oracle (C), Newton-Schulz as the reference computes it
+    on the CPU (gefen_muon.py:16-51: torch bf16 tensors, X @ X.T and two addmm
+    per iteration, each product accumulated in float32 by torch's CPU GEMM and
+    rounded to bf16, on torch's intra-op threads), the parameter update from the
+    oracle (gefen_muon.py:325-329)."""
     from oracle import oracle as orc
 
-    try:
-        from threadpoolctl import threadpool_info
-        blas = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
-    except ImportError:
-        blas = 1
+    threads = torch.get_num_threads()
     cb = opt._gefen_codebook.detach().cpu().numpy().astype(np.float32)
     g0 = opt.param_groups[0]
-    coeffs, steps, eps = tuple(g0["ns_coefficients"]), g0["ns_steps"], g0["eps"]
+    (a, b, c), steps, eps = tuple(g0["ns_coefficients"]), g0["ns_steps"], g0["eps"]
 
     def ns_flops(shape):
         m, n = min(shape), max(shape)
         return steps * 2.0 * (m * m * n + m * m * m + m * m * n)
 
-    # the first q_proj-like (square) and k_proj-like (1024 x 2048) matrices
-    sample = [next(i for i, (_, p) in enumerate(params) if p.shape[0] == p.shape[1]),
-              next(i for i, (_, p) in enumerate(params) if p.shape[0] < p.shape[1])]
+    def newton_schulz_cpu(u_bits, shape):
+        x = torch.from_numpy(u_bits.view(np.int16).reshape(shape)).view(torch.bfloat16)
+        if shape[0] > shape[1]:
+            x = x.T
+        x = x / x.norm().clamp(min=eps)
+        for _ in range(steps):
+            am = x @ x.T
+            bm = torch.addmm(am, am, am, beta=b, alpha=c)
+            x = torch.addmm(x, bm, x, beta=a)
+        if shape[0] > shape[1]:
+            x = x.T
+        return x.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+
+    sample, seen = [], set()
+    for i, (_, p) in enumerate(params):
+        if tuple(p.shape) not in seen:
+            seen.add(tuple(p.shape))
+            sample.append(i)
     host = []
     for i in sample:
         _, p = params[i]
@@ -478,21 +491,22 @@ def cpu_baseline_muon(opt, params, budget_s=20.0):
     while elapsed < budget_s and reps < 5:
         t0 = time.perf_counter()
         for i, pp, gg, tstate in host:
-            _, p = params[i]
+            shape = tuple(params[i][1].shape)
             blend = orc.muon_momentum(gg, "bf16", tstate, cb, g0["momentum"], g0["nesterov"])
-            u = orc.newton_schulz_bf16(orc.to_f32(blend, "bf16").reshape(tuple(p.shape)), coeffs, steps, eps)
-            orc.muon_apply(pp, orc.from_f32(u, "bf16"), "bf16", tuple(p.shape), g0["lr"], g0["weight_decay"],
-                           orc.adjust_lr(g0["lr"], g0["adjust_lr_fn"], tuple(p.shape)))
+            u = newton_schulz_cpu(blend, shape)
+            orc.muon_apply(pp, u, "bf16", shape, g0["lr"], g0["weight_decay"],
+                           orc.adjust_lr(g0["lr"], g0["adjust_lr_fn"], shape))
         elapsed += time.perf_counter() - t0
         reps += 1
     per_rep = elapsed / reps
     scale = sum(ns_flops(tuple(p.shape)) for _, p in params) / sum(ns_flops(tuple(params[i][1].shape))
                                                                     for i in sample)
     return {"value": round(per_rep * scale * 1000.0, 1), "unit": "ms per full step (scaled by Newton-Schulz flops)",
-            "cores": blas, "kind": "port",
-            "sample": "{} matrices ({}), {} repetitions of the oracle GefenMuon step (numpy float64 products on {} "
-                      "BLAS threads), scaled by Newton-Schulz flops to all {} matrices".format(
-                          len(sample), ", ".join("{}x{}".format(*params[i][1].shape) for i in sample), reps, blas,
+            "cores": threads, "kind": "port",
+            "sample": "one matrix of each shape ({}), {} repetitions of the reference CPU path's GefenMuon step "
+                      "(Newton-Schulz as torch bf16 CPU products on {} intra-op threads, momentum and update from "
+                      "the C oracle), scaled by Newton-Schulz flops to all {} matrices".format(
+                          ", ".join("{}x{}".format(*params[i][1].shape) for i in sample), reps, threads,
                           len(params))}
 
 

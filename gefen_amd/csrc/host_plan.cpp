@@ -89,6 +89,9 @@ class PlanCore {
         gptr_.resize(n);
         step_.resize(n);
         hyper_.resize(n);
+        hcache_.resize(n);
+        hcache_ok_.assign(n, false);
+        hobj_.resize(n);
     }
 
     // table: address of the task table (rows of `stride` bytes); cols: byte offsets
@@ -129,7 +132,7 @@ class PlanCore {
                     return false;
                 if (reinterpret_cast<uintptr_t>(t.data_ptr()) != pptr_[k] || !t.is_contiguous()) return false;
                 if (hyper && !have_hyper) {
-                    if (!group_hyper(group, h)) return false;
+                    if (!group_hyper_cached(group, k, h)) return false;
                     have_hyper = true;
                 }
                 gptr_[k] = reinterpret_cast<uint64_t>(g.data_ptr());
@@ -182,9 +185,49 @@ class PlanCore {
         return true;
     }
 
+    // refresh(), then, when it succeeded, the step itself: run_fn is the address of
+    // the C ABI's gefen_step_plan_run, called with (plan, table, number of rows,
+    // stream) while the table is fresh, so a cached step costs one call from
+    // Python.  Returns -1 when the plan no longer applies (nothing was changed or
+    // launched), else gefen_step_plan_run's status.
+    int step(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols, uintptr_t steps_out,
+             uintptr_t run_fn, uintptr_t plan, uintptr_t stream) {
+        if (!run_fn || !plan) throw py::value_error("PlanCore.step: null run function or plan");
+        if (!refresh(param_groups, table, stride, cols, steps_out)) return -1;
+        using RunFn = int (*)(void*, const void*, int, void*);
+        return reinterpret_cast<RunFn>(run_fn)(reinterpret_cast<void*>(plan), reinterpret_cast<const void*>(table),
+                                               static_cast<int>(params_.size()), reinterpret_cast<void*>(stream));
+    }
+
     size_t size() const { return params_.size(); }
 
    private:
+    // group_hyper with the result kept per parameter k: when the five values are
+    // the same Python float or int objects as at the last refresh (immutable, and
+    // held here so their addresses cannot be reused), the kept doubles are reused.
+    bool group_hyper_cached(PyObject* group, size_t k, std::array<double, 5>& h) {
+        PyObject* keys[5] = {key_lr_, key_beta1_, key_beta2_, key_eps_, key_wd_};
+        PyObject* vals[5];
+        bool same = hcache_ok_[k];
+        for (int c = 0; c < 5; ++c) {
+            vals[c] = PyDict_GetItem(group, keys[c]);
+            if (!vals[c]) return false;
+            same = same && vals[c] == hobj_[k][c].ptr() && (PyFloat_CheckExact(vals[c]) || PyLong_CheckExact(vals[c]));
+        }
+        if (same) {
+            h = hcache_[k];
+            return true;
+        }
+        if (!group_hyper(group, h)) {
+            hcache_ok_[k] = false;
+            return false;
+        }
+        for (int c = 0; c < 5; ++c) hobj_[k][c] = py::reinterpret_borrow<py::object>(vals[c]);
+        hcache_[k] = h;
+        hcache_ok_[k] = true;
+        return true;
+    }
+
     // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group,
     // the weight decay as the kernels take it.  For a float32 tensor lr with
     // weight decay, torch forms the decay factor in float32,
@@ -236,6 +279,9 @@ class PlanCore {
     std::vector<uint64_t> gptr_;
     std::vector<long long> step_;
     std::vector<std::array<double, 5>> hyper_;
+    std::vector<std::array<double, 5>> hcache_;  // group_hyper_cached: kept results
+    std::vector<bool> hcache_ok_;
+    std::vector<std::array<py::object, 5>> hobj_;
 };
 
 }  // namespace
@@ -252,5 +298,6 @@ PYBIND11_MODULE(_gefen_host, m) {
     py::class_<PlanCore>(m, "PlanCore")
         .def(py::init<py::list, py::list, py::tuple>())
         .def("refresh", &PlanCore::refresh)
+        .def("step", &PlanCore::step)
         .def("__len__", &PlanCore::size);
 }

@@ -434,7 +434,7 @@ void plan_luts(const std::vector<PendingStep>& pend, LutPlan& lp) {
 
 // Build the planned tables at base (lp.total floats of device memory) on st and
 // point the tasks at them.
-int build_luts(std::vector<PendingStep>& pend, const LutPlan& lp, float* base, hipStream_t st) {
+int launch_luts(const LutPlan& lp, float* base, hipStream_t st) {
     for (size_t j = 0; j < lp.keys.size(); ++j) {
         StepTask t;
         memset(&t, 0, sizeof(t));
@@ -448,9 +448,19 @@ int build_luts(std::vector<PendingStep>& pend, const LutPlan& lp, float* base, h
         int rc = launch_status("gefen stepsize table");
         if (rc) return rc;
     }
+    return GEFEN_OK;
+}
+
+// Point the tasks at their tables in base.
+void assign_luts(std::vector<PendingStep>& pend, const LutPlan& lp, float* base) {
     for (size_t i = 0; i < pend.size(); ++i)
         if (lp.which[i] >= 0) pend[i].task.lut = base + lp.off[(size_t)lp.which[i]];
-    return GEFEN_OK;
+}
+
+int build_luts(std::vector<PendingStep>& pend, const LutPlan& lp, float* base, hipStream_t st) {
+    int rc = launch_luts(lp, base, st);
+    if (rc == GEFEN_OK) assign_luts(pend, lp, base);
+    return rc;
 }
 
 // Device of a stream (the current device for the null stream).
@@ -731,6 +741,7 @@ struct gefen_step_plan {
     std::vector<StepLaunch> launches;
     std::vector<int> slot;               // launch * kMaxBatch + position of each pending task
     LutPlan lp;                          // stepsize tables of the current run
+    std::vector<int> launch_key;         // stepsize-table key of each launch in the current run
     SideStream* side = nullptr;
     bool timing = false, timed = false;
     hipEvent_t t0 = nullptr, t1 = nullptr;
@@ -749,7 +760,17 @@ bool same_tensors(const gefen_step_task& a, const gefen_step_task& b) {
 
 // The plan's fast path: a GEFEN_* status, or -1 when the rows do not fit the
 // plan (then nothing was launched).
+// The hyperparameters and bias corrections of a task row, as compared between rows.
+bool same_scalars(const gefen_step_task& a, const gefen_step_task& b) {
+    return a.beta1 == b.beta1 && a.beta2 == b.beta2 && a.lr == b.lr && a.eps == b.eps &&
+           a.weight_decay == b.weight_decay && a.bias_correction_1 == b.bias_correction_1 &&
+           a.bias_correction_2 == b.bias_correction_2;
+}
+
 int plan_run_fast(gefen_step_plan& P, const gefen_step_task* tasks, hipStream_t st) {
+    // rows of one group share their scalars: the float forms are computed once per run of equal rows
+    const gefen_step_task* prev = nullptr;
+    const StepTask* prev_t = nullptr;
     for (size_t i = 0; i < P.pend.size(); ++i) {
         const gefen_step_task& in = tasks[P.row[i]];
         if (!same_tensors(in, P.shape[P.row[i]]) || !in.grad || !aligned(in.grad, P.galign[i])) return -1;
@@ -757,41 +778,100 @@ int plan_run_fast(gefen_step_plan& P, const gefen_step_task* tasks, hipStream_t 
         if (rc) return rc;
         StepTask& t = P.pend[i].task;
         t.g = in.grad;
-        set_step_scalars(in, t);
+        if (prev && same_scalars(in, *prev)) {
+            t.b1c = prev_t->b1c; t.b2 = prev_t->b2; t.omb2 = prev_t->omb2; t.sqrt_bc2 = prev_t->sqrt_bc2;
+            t.eps = prev_t->eps; t.inv_bc1 = prev_t->inv_bc1; t.lr = prev_t->lr; t.do_wd = prev_t->do_wd;
+            t.wdf = prev_t->wdf;
+        } else {
+            set_step_scalars(in, t);
+        }
         t.lut = nullptr;
+        prev = &in;
+        prev_t = &t;
     }
     // every row that must be stepped as a no-op (numel 0) is still empty
     for (int r = 0; r < P.ntasks; ++r)
         if (tasks[r].numel != P.shape[r].numel) return -1;
     plan_luts(P.pend, P.lp);
     // one stepsize table per launch, as the grouping assumed
-    {
-        std::vector<int> key_of_launch(P.launches.size(), -2);
-        for (size_t i = 0; i < P.pend.size(); ++i) {
-            int& k = key_of_launch[(size_t)(P.slot[i] / kMaxBatch)];
-            if (k == -2) k = P.lp.which[i];
-            else if (k != P.lp.which[i]) return -1;
-        }
+    P.launch_key.assign(P.launches.size(), -2);
+    for (size_t i = 0; i < P.pend.size(); ++i) {
+        int& k = P.launch_key[(size_t)(P.slot[i] / kMaxBatch)];
+        if (k == -2) k = P.lp.which[i];
+        else if (k != P.lp.which[i]) return -1;
     }
-    const bool timing = P.timing;
-    if (timing && hipEventRecord(P.t0, st) != hipSuccess) return launch_status("hipEventRecord(step plan)");
+    // stepsize tables: reserve the pool (ordered after its last use on another
+    // stream) and point the tasks at their tables before the launch tables are filled
     int rc = GEFEN_OK;
     LutPool* pool = nullptr;
-    std::unique_lock<std::mutex> lock;
+    std::unique_lock<std::mutex> pool_lock;
     if (!P.lp.keys.empty()) {
         pool = &g_lut_pool[P.dev];
-        lock = std::unique_lock<std::mutex>(pool->m);
+        pool_lock = std::unique_lock<std::mutex>(pool->m);
         rc = lut_pool_reserve(*pool, P.dev, P.lp.total, st);
         if (rc) return rc;
-        rc = build_luts(P.pend, P.lp, pool->buf, st);
+        assign_luts(P.pend, P.lp, pool->buf);
     }
-    if (rc == GEFEN_OK) {
-        for (size_t i = 0; i < P.pend.size(); ++i) {
-            const int q = P.slot[i];
-            P.launches[(size_t)(q / kMaxBatch)].b.t[q % kMaxBatch] = P.pend[i].task;
+    for (size_t i = 0; i < P.pend.size(); ++i) {
+        const int q = P.slot[i];
+        P.launches[(size_t)(q / kMaxBatch)].b.t[q % kMaxBatch] = P.pend[i].task;
+    }
+    // Issue order, so that the first large launch goes out as early as possible:
+    // the side stream's fork event (recorded before any launch, so the side
+    // stream waits only for the work before this step), the large launches on st
+    // with the stepsize tables built right before the first launch that reads
+    // them, then the side stream's wait and the small launches (tables built
+    // before the fork when a small launch reads them), and the join.
+    bool any_small = false, any_large = false, small_lut = false;
+    for (size_t l = 0; l < P.launches.size(); ++l) {
+        const bool small = P.launches[l].elems < kSmallLaunchElems;
+        (small ? any_small : any_large) = true;
+        small_lut = small_lut || (small && P.launches[l].b.t[0].lut);
+    }
+    SideStream* side = (any_small && any_large) ? P.side : nullptr;
+    const bool timing = P.timing;
+    if (timing && hipEventRecord(P.t0, st) != hipSuccess) rc = launch_status("hipEventRecord(step plan)");
+    bool luts_built = pool == nullptr;
+    if (rc == GEFEN_OK && !luts_built && side && small_lut) {
+        rc = launch_luts(P.lp, pool->buf, st);
+        luts_built = true;
+    }
+    std::unique_lock<std::mutex> side_lock;
+    if (rc == GEFEN_OK && side) {
+        side_lock = std::unique_lock<std::mutex>(side->m);
+        if (hipEventRecord(side->fork, st) != hipSuccess) rc = launch_status("gefen step fork");
+    }
+    for (size_t l = 0; rc == GEFEN_OK && l < P.launches.size(); ++l) {
+        const StepLaunch& L = P.launches[l];
+        if (side && L.elems < kSmallLaunchElems) continue;
+        if (!luts_built && L.b.t[0].lut) {
+            rc = launch_luts(P.lp, pool->buf, st);
+            luts_built = true;
+            if (rc) break;
         }
-        rc = issue_launches(P.launches, st, true, P.side);
+        hipError_t e = dispatch_step(L.key, L.b, L.wg, st);
+        if (e != hipSuccess) rc = hip_status(e, "gefen step launch");
     }
+    if (side) {
+        bool waited = false;
+        if (rc == GEFEN_OK) {
+            if (hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess) rc = launch_status("gefen step fork");
+            else waited = true;
+        }
+        for (size_t l = 0; rc == GEFEN_OK && l < P.launches.size(); ++l) {
+            const StepLaunch& L = P.launches[l];
+            if (L.elems >= kSmallLaunchElems) continue;
+            hipError_t e = dispatch_step(L.key, L.b, L.wg, side->s);
+            if (e != hipSuccess) rc = hip_status(e, "gefen step launch");
+        }
+        // join even after a failed launch: st stays ordered after what the side stream queued
+        if (waited) {
+            const hipError_t e1 = hipEventRecord(side->join, side->s);
+            const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(st, side->join, 0) : e1;
+            if (e2 != hipSuccess && rc == GEFEN_OK) rc = hip_status(e2, "gefen step join");
+        }
+    }
+    // recorded after the join: covers every launch that reads the stepsize tables
     if (pool) rc = pool->order.record(st, rc);
     if (timing) {
         hipError_t e = hipEventRecord(P.t1, st);

@@ -258,6 +258,17 @@ def _flat_with_data(grad: torch.Tensor) -> torch.Tensor:
     return flat
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(index: int) -> int:
+    """The hipStream_t of the current stream of device `index` (without building a
+    torch.cuda.Stream object when torch offers the raw handle)."""
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
 def _local(tensor):
     if hasattr(tensor, "to_local"):
         tensor = tensor.to_local()
@@ -285,7 +296,7 @@ class _StepPlan:
     __slots__ = ("params", "pptr", "numel", "gdtype", "states", "state_keys", "srefs", "groups", "tasks", "device",
                  "dev_index",
                  "grads", "gptr", "distinct", "group_index", "hyper", "core", "steps", "columns", "tables", "handle",
-                 "lib")
+                 "lib", "run_fn", "tptr")
 
     def __init__(self, opt, items, tasks, device, tables):
         self.params = [it[1] for it in items]
@@ -321,6 +332,26 @@ class _StepPlan:
             _lib.check(self.lib.gefen_step_plan_create(self.tasks.ctypes.data, len(self.tasks), tables.data_ptr(),
                                                        ctypes.byref(handle)), "gefen_step_plan_create")
         self.handle = handle.value
+        self.run_fn = ctypes.cast(self.lib.gefen_step_plan_run, ctypes.c_void_p).value
+        self.tptr = self.tasks.ctypes.data
+
+    def step(self, opt, tables, stream) -> bool:
+        """One cached step on `stream` (the plan's device current): the checks and
+        refresh of ``refresh``, then the kept launches; False (nothing changed or
+        launched) when the plan no longer applies.  With the host extension both
+        happen in one call (PlanCore.step)."""
+        if self.core is not None and tables is self.tables:
+            rc = self.core.step(opt.param_groups, self.tptr, self.tasks.itemsize, self.columns,
+                                self.steps.ctypes.data, self.run_fn, self.handle, stream)
+            if rc == -1:
+                return False
+            _lib.check(rc, "gefen_step_plan_run")
+            return True
+        tasks = self.refresh(opt)
+        if tasks is None:
+            return False
+        self.run(tasks, tables, stream)
+        return True
 
     def __del__(self):
         if getattr(self, "handle", None):
@@ -841,17 +872,17 @@ class Gefen(torch.optim.Optimizer):
         only refreshes gradient addresses, step counts and hyperparameters.
         """
         plan = self._plan
-        tasks = plan.refresh(self) if plan is not None else None
-        if tasks is None:
-            self._plan = None
-            self._step_all_build()
-            return
-        tables = self._codebook_tables()
-        if torch.cuda.current_device() == plan.dev_index:
-            plan.run(tasks, tables, torch.cuda.current_stream().cuda_stream)
-        else:
-            with torch.cuda.device(plan.device):
-                plan.run(tasks, tables, torch.cuda.current_stream(plan.device).cuda_stream)
+        if plan is not None:
+            tables = self._codebook_tables()
+            if torch.cuda.current_device() == plan.dev_index:
+                done = plan.step(self, tables, _stream_handle(plan.dev_index))
+            else:
+                with torch.cuda.device(plan.device):
+                    done = plan.step(self, tables, _stream_handle(plan.dev_index))
+            if done:
+                return
+        self._plan = None
+        self._step_all_build()
 
     def _step_all_build(self) -> None:
         """_step_all from scratch: resolves every tensor, fills the task table and,

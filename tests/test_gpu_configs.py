@@ -232,7 +232,9 @@ def _free_running_bf16(config, steps):
     ref_cb = orc.learn_codebook([(g, "bf16", P) for g, P in zip(grads, ref_periods)])
     np.testing.assert_array_equal(opt._gefen_codebook.detach().cpu().numpy(), ref_cb)
     print("periods and codebook match the oracle", flush=True)
-    sample = _sample(params, opt)
+    # the embedding, a block-row and a period-one matrix, a norm (the lm_head has the
+    # embedding's shape and period: left out to keep the run within two minutes)
+    sample = [i for i in _sample(params, opt) if i != len(params) - 1]
     kinds = {("one" if periods[i] == 1 else "rows") if params[i][1].dim() == 2 else "vector" for i in sample}
     assert {"rows", "one", "vector"} <= kinds, sample
     arrs = [{"p": _initial(cfg, params, i), "dtype": "bf16", "shape": tuple(params[i][1].shape), "lr": 1e-3,

@@ -163,3 +163,15 @@ def test_step_plan_rejects_invalid_rows_like_step_tasks():
                                       ctypes.byref(plan)) == _lib.GEFEN_EINVAL
     assert plan.value is None
     torch.cuda.synchronize()
+
+
+def test_stream_handle_is_the_current_stream():
+    """The optimizer's cached step launches on the raw handle of torch's current
+    stream, on the default stream and inside a torch.cuda.stream context."""
+    from gefen_amd.gefen import _stream_handle
+
+    assert _stream_handle(0) == torch.cuda.current_stream(0).cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert _stream_handle(0) == s.cuda_stream == torch.cuda.current_stream().cuda_stream
+    assert _stream_handle(0) == torch.cuda.current_stream(0).cuda_stream
