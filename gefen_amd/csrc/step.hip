@@ -371,6 +371,8 @@ int make_step_task(const gefen_step_task& in, int mode, const float* stepsize, P
     if (p1 && R == 0) return fail_inval("period_one_divisor %lld is too large", (long long)rowlen);
     // row tables pay off when a row has at least as many elements as codewords per lane group
     const int tab = (R != 0 && l2 >= 5 && !p1) ? 1 : 0;
+    // the kernels keep one row table per wave when R >= 2 (whole-wave rows)
+    if (tab && R >= 2 && l2 != 6) return fail_inval("internal: row tables of a %d-lane row", 1 << l2);
     Key k{in.param_dtype, in.state_dtype, R == 0 ? 1 : W, R, p1 ? 1 : 0, tab};
     StepTask& t = out.task;
     memset(&t, 0, sizeof(t));
@@ -1105,6 +1107,8 @@ int make_muon_task(const gefen_muon_task& in, PendingMuon& out) {
     if (R == 4 && W == 8 && ((nvec + (1LL << l2) - 1) >> l2) == 3) R = 3;
     // row tables pay off for whole-wave rows (measured: 5% faster there, none for 32-lane rows)
     const int tab = (R != 0 && l2 >= GEFEN_MUON_TAB_LOG2) ? 1 : 0;
+    // k_muon keeps one row table per wave: whole-wave rows only
+    static_assert(GEFEN_MUON_TAB_LOG2 >= 6, "GefenMuon row tables need whole-wave rows");
     Key k{in.grad_dtype, in.state_dtype, R == 0 ? 1 : W, R, 0, tab};
     MuonTask& t = out.task;
     memset(&t, 0, sizeof(t));

@@ -391,7 +391,12 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
     // workgroup per CU
     constexpr bool kFine = sizeof(D) == 2;
     __shared__ LdsTables<kFine> L;
-    __shared__ float row_tab[TAB ? kStepWaves : 1][TAB ? 2 : 1][2][256];
+    // row tables of the wave's rows: rows of at least two vectors per lane own a
+    // whole wave (64 lanes), so one slot per wave; single-vector rows may take 32
+    // lanes, two rows per wave (make_step_task keeps to this).  The smaller LDS
+    // footprint lets more workgroups share a CU.
+    constexpr int kRowSlots = (TAB && R == 1) ? 2 : 1;
+    __shared__ float row_tab[TAB ? kStepWaves : 1][kRowSlots][2][256];
     __shared__ __attribute__((aligned(16))) float root_lds[kRoot ? kRootTab : 4];
     // every task of a launch has the same stepsize table (flush_steps)
     const float* root_src = kRoot ? B.t[0].lut : nullptr;
@@ -410,8 +415,8 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
     const int lir = lane & (lpr - 1);
     const int sub = lane >> T.lpr_log2;
     const int64_t lw = blockIdx.x - B.wg_begin[ti];
-    float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
-    float* utab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
+    float* ctab = row_tab[TAB ? wave : 0][kRowSlots == 2 ? (sub & 1) : 0][0];
+    float* utab = row_tab[TAB ? wave : 0][kRowSlots == 2 ? (sub & 1) : 0][1];
 
     constexpr int kIt = step_iter<P1>();
     for (int it = 0; it < kIt; ++it) {
@@ -717,7 +722,9 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     constexpr bool kNb = std::is_same<D, bf16_t>::value;  // bf16 quotients: the nb16 table
     constexpr bool kPk = kNb && W % 2 == 0;                // bf16 pairs: packed conversions
     __shared__ LdsTables<false> L;
-    __shared__ float row_tab[TAB ? 4 : 1][TAB ? 2 : 1][2][256];
+    // one row table per wave: row tables are used for whole-wave rows only
+    // (make_muon_task keeps to this)
+    __shared__ float row_tab[TAB ? 4 : 1][2][256];
     __shared__ __attribute__((aligned(16))) uint8_t nb16[kNb ? kNb16Bytes : 16];
     int K;
     load_tables<D, kThreads, kNb>(L, B.tables, K, nullptr, nullptr, nb16);
@@ -731,8 +738,8 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
     const int lir = lane & (lpr - 1);
     const int sub = lane >> T.lpr_log2;
     const int64_t lw = blockIdx.x - B.wg_begin[ti];
-    float* ctab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][0];
-    float* otab = row_tab[TAB ? wave : 0][TAB ? (sub & 1) : 0][1];
+    float* ctab = row_tab[TAB ? wave : 0][0];
+    float* otab = row_tab[TAB ? wave : 0][1];
     float wsq = 0.0f;  // this lane's sum of squares of the outputs it wrote
 
     for (int it = 0; it < kMuonIter; ++it) {
