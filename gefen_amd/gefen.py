@@ -354,9 +354,13 @@ class _StepPlan:
         return True
 
     def __del__(self):
-        if getattr(self, "handle", None):
-            self.lib.gefen_step_plan_destroy(self.handle)
+        handle = getattr(self, "handle", None)
+        if handle:
             self.handle = None
+            try:
+                self.lib.gefen_step_plan_destroy(handle)
+            except Exception:  # interpreter shutdown: the library may already be gone
+                pass
 
     def run(self, tasks, tables, stream) -> None:
         """Steps the refreshed table on `stream` (the plan's device current):

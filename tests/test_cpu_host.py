@@ -61,6 +61,24 @@ def test_entry_points_reject_invalid_arguments_without_a_device():
         _lib.check(lib.gefen_gemm_bf16_nt_batched(256, 320, 0, 256, 320, 0, 256, 320, 0, None, 0, 0, None, 0, 0,
                                                   0, 1, 320, 320, 320, 1.0, 0.0, 0, None))
     assert lib.gefen_exact_dp_workspace_size(4096, 256) > 256 * 4097 * 12
+    # the step plan refuses a null result pointer, a negative task count and null
+    # tables before touching a device
+    import ctypes
+
+    plan = ctypes.c_void_p()
+    with pytest.raises(ValueError, match="null plan pointer"):
+        _lib.check(lib.gefen_step_plan_create(None, 0, 1, None))
+    with pytest.raises(ValueError, match="invalid task array"):
+        _lib.check(lib.gefen_step_plan_create(None, -1, 1, ctypes.byref(plan)))
+    with pytest.raises(ValueError, match="null codebook tables"):
+        _lib.check(lib.gefen_step_plan_create(None, 0, None, ctypes.byref(plan)))
+    assert plan.value is None
+    with pytest.raises(ValueError, match="null step plan"):
+        _lib.check(lib.gefen_step_plan_run(None, None, 0, None))
+    with pytest.raises(ValueError, match="null step plan"):
+        _lib.check(lib.gefen_step_plan_time_runs(None, 1))
+    lib.gefen_step_plan_destroy(None)  # a null plan is ignored
+    assert lib.gefen_device_allocations() == 0  # nothing allocated without a device
 
 
 def test_batched_newton_schulz_shape_predicate_matches_the_byte_limit():
