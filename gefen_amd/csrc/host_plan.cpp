@@ -33,6 +33,19 @@ namespace py = pybind11;
 
 namespace {
 
+// CPython 3.6 - 3.11 give every dict a version tag that changes with each
+// modification of that dict (PEP 509).  Where it exists, a param group or state
+// dict whose tag equals the one recorded at the last refresh still holds the
+// same value objects, so their lookups are skipped; elsewhere every value is
+// looked up each time.
+#if PY_VERSION_HEX >= 0x03060000 && PY_VERSION_HEX < 0x030C0000
+constexpr bool kDictVersion = true;
+inline uint64_t dict_version(PyObject* d) { return reinterpret_cast<PyDictObject*>(d)->ma_version_tag; }
+#else
+constexpr bool kDictVersion = false;
+inline uint64_t dict_version(PyObject*) { return 0; }
+#endif
+
 // interned dict keys, created once at module import
 PyObject* key_params_;
 PyObject* key_step_;
@@ -89,9 +102,8 @@ class PlanCore {
         gptr_.resize(n);
         step_.resize(n);
         hyper_.resize(n);
-        hcache_.resize(n);
-        hcache_ok_.assign(n, false);
-        hobj_.resize(n);
+        sver_.assign(n, 0);
+        committed_.assign(n, 0);
     }
 
     // table: address of the task table (rows of `stride` bytes); cols: byte offsets
@@ -111,11 +123,22 @@ class PlanCore {
         const size_t n = params_.size();
         size_t k = 0;
         const Py_ssize_t ngroups = PyList_GET_SIZE(param_groups.ptr());
+        if ((size_t)ngroups > gcache_.size()) gcache_.resize((size_t)ngroups);
         for (Py_ssize_t gi = 0; gi < ngroups; ++gi) {
             PyObject* group = PyList_GET_ITEM(param_groups.ptr(), gi);
             if (!PyDict_Check(group)) return false;
-            PyObject* plist = PyDict_GetItem(group, key_params_);
+            GroupCache& gc = gcache_[(size_t)gi];
+            // the same group dict, unmodified since the last refresh: the same "params"
+            // list object and the same hyperparameter objects
+            const bool same_group = kDictVersion && gc.group.ptr() == group && gc.ver == dict_version(group);
+            PyObject* plist = same_group ? gc.params.ptr() : PyDict_GetItem(group, key_params_);
             if (!plist || !PyList_Check(plist)) return false;
+            if (!same_group) {
+                gc.group = py::reinterpret_borrow<py::object>(group);
+                gc.params = py::reinterpret_borrow<py::object>(plist);
+                gc.ver = dict_version(group);
+                gc.hyper_ok = false;
+            }
             const Py_ssize_t np = PyList_GET_SIZE(plist);
             bool have_hyper = false;
             std::array<double, 5> h{};
@@ -132,7 +155,16 @@ class PlanCore {
                     return false;
                 if (reinterpret_cast<uintptr_t>(t.data_ptr()) != pptr_[k] || !t.is_contiguous()) return false;
                 if (hyper && !have_hyper) {
-                    if (!group_hyper_cached(group, k, h)) return false;
+                    if (gc.hyper_ok) {
+                        h = gc.h;
+                    } else {
+                        bool immutable = false;
+                        if (!group_hyper(group, h, &immutable)) return false;
+                        // numbers are immutable: kept while the group dict is unmodified (a
+                        // 0-d tensor lr can change in place and is read every time)
+                        gc.h = h;
+                        gc.hyper_ok = kDictVersion && immutable;
+                    }
                     have_hyper = true;
                 }
                 gptr_[k] = reinterpret_cast<uint64_t>(g.data_ptr());
@@ -143,6 +175,12 @@ class PlanCore {
         if (k != n) return false;
         for (k = 0; k < n; ++k) {
             PyObject* st = states_[k].ptr();
+            // unmodified since this refresh last wrote "step": same state tensors, and
+            // "step" is the value written then
+            if (kDictVersion && sver_[k] != 0 && sver_[k] == dict_version(st)) {
+                step_[k] = committed_[k] + 1;
+                continue;
+            }
             for (size_t j = 0; j < skeys_.size(); ++j)
                 if (PyDict_GetItem(st, skeys_[j].ptr()) != srefs_[k][j].ptr()) return false;
             PyObject* s = PyDict_GetItem(st, key_step_);
@@ -179,6 +217,8 @@ class PlanCore {
             if (!v) throw py::error_already_set();
             const int rc = PyDict_SetItem(states_[k].ptr(), key_step_, v);
             Py_DECREF(v);
+            sver_[k] = rc == 0 ? dict_version(states_[k].ptr()) : 0;
+            committed_[k] = step_[k];
             if (rc != 0) throw py::error_already_set();
             steps[k] = step_[k];
         }
@@ -202,32 +242,6 @@ class PlanCore {
     size_t size() const { return params_.size(); }
 
    private:
-    // group_hyper with the result kept per parameter k: when the five values are
-    // the same Python float or int objects as at the last refresh (immutable, and
-    // held here so their addresses cannot be reused), the kept doubles are reused.
-    bool group_hyper_cached(PyObject* group, size_t k, std::array<double, 5>& h) {
-        PyObject* keys[5] = {key_lr_, key_beta1_, key_beta2_, key_eps_, key_wd_};
-        PyObject* vals[5];
-        bool same = hcache_ok_[k];
-        for (int c = 0; c < 5; ++c) {
-            vals[c] = PyDict_GetItem(group, keys[c]);
-            if (!vals[c]) return false;
-            same = same && vals[c] == hobj_[k][c].ptr() && (PyFloat_CheckExact(vals[c]) || PyLong_CheckExact(vals[c]));
-        }
-        if (same) {
-            h = hcache_[k];
-            return true;
-        }
-        if (!group_hyper(group, h)) {
-            hcache_ok_[k] = false;
-            return false;
-        }
-        for (int c = 0; c < 5; ++c) hobj_[k][c] = py::reinterpret_borrow<py::object>(vals[c]);
-        hcache_[k] = h;
-        hcache_ok_[k] = true;
-        return true;
-    }
-
     // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group,
     // the weight decay as the kernels take it.  For a float32 tensor lr with
     // weight decay, torch forms the decay factor in float32,
@@ -237,12 +251,15 @@ class PlanCore {
     // rounds to f exactly (gefen.py's _kernel_weight_decay does the same).  A
     // tensor lr of a 16-bit dtype with weight decay, lr <= 0 or f zero or not
     // finite is refused: the Python step applies torch's factor before the launch.
-    bool group_hyper(PyObject* group, std::array<double, 5>& h) {
+    // immutable: set when all five values are Python floats or ints.
+    bool group_hyper(PyObject* group, std::array<double, 5>& h, bool* immutable = nullptr) {
         PyObject* keys[5] = {key_lr_, key_beta1_, key_beta2_, key_eps_, key_wd_};
         int lr_kind = 0;  // 0: number or float64 tensor, 1: float32 tensor, 2: other tensor
+        bool numbers = true;
         for (int c = 0; c < 5; ++c) {
             PyObject* v = PyDict_GetItem(group, keys[c]);
             if (!v) return false;
+            numbers = numbers && (PyFloat_CheckExact(v) || PyLong_CheckExact(v));
             if (c == 0 && THPVariable_Check(v)) {
                 const at::ScalarType st = THPVariable_Unpack(v).scalar_type();
                 lr_kind = st == at::kDouble ? 0 : (st == at::kFloat ? 1 : 2);
@@ -259,6 +276,7 @@ class PlanCore {
             h[c] = PyFloat_AS_DOUBLE(f);
             Py_DECREF(f);
         }
+        if (immutable) *immutable = numbers;
         if (lr_kind == 0 || !(h[4] > 0.0)) return true;
         if (lr_kind != 1 || !(h[0] > 0.0)) return false;
         const volatile float prod = (float)h[0] * (float)h[4];  // volatile: each op rounded to float
@@ -279,9 +297,17 @@ class PlanCore {
     std::vector<uint64_t> gptr_;
     std::vector<long long> step_;
     std::vector<std::array<double, 5>> hyper_;
-    std::vector<std::array<double, 5>> hcache_;  // group_hyper_cached: kept results
-    std::vector<bool> hcache_ok_;
-    std::vector<std::array<py::object, 5>> hobj_;
+    // per param group position: the group dict and its version at the last refresh,
+    // its "params" list, and its hyperparameters when they are kept (numbers)
+    struct GroupCache {
+        py::object group, params;
+        uint64_t ver = 0;
+        bool hyper_ok = false;
+        std::array<double, 5> h{};
+    };
+    std::vector<GroupCache> gcache_;
+    std::vector<uint64_t> sver_;          // version of each state dict after its "step" was written (0: none)
+    std::vector<long long> committed_;    // the "step" value written then
 };
 
 }  // namespace

@@ -249,6 +249,28 @@ def test_plan_core_checks_and_commits_only_when_the_plan_applies():
                     lambda: groups[1].__setitem__("lr", 2e-3))
     assert [st["step"] for st in states] == [12, 13, 13] and steps.tolist() == [12, 13, 13]
     assert table["bias_correction_1"].tolist() == [1 - 0.9 ** 12, 1 - 0.9 ** 13, 1 - 0.8 ** 13]
+    # values changed without a new dict entry are still seen: a 0-d lr tensor changed
+    # in place, a state "step" written by the user, a state tensor replaced
+    lr64 = torch.tensor(2e-3, dtype=torch.float64)
+    groups[1]["lr"] = lr64
+    assert refresh(groups) and table["lr"][2] == 2e-3
+    lr64.fill_(3e-3)
+    assert refresh(groups) and table["lr"][2] == 3e-3
+    groups[1]["lr"] = 2e-3
+    s0 = states[0]["step"]
+    assert refresh(groups) and refresh(groups) and states[0]["step"] == s0 + 2
+    states[0]["step"] = 100
+    assert refresh(groups) and states[0]["step"] == 101 and steps[0] == 101
+    states[0]["step"] = s0 + 3
+    vm0 = states[0]["vmean"]
+    states[0]["vmean"] = vm0.clone()
+    assert not refresh(groups)
+    states[0]["vmean"] = vm0
+    assert refresh(groups) and states[0]["step"] == s0 + 4
+    states[0]["step"], states[1]["step"], states[2]["step"] = 12, 13, 13
+    assert refresh(groups)
+    for st in states:
+        st["step"] -= 1
     # a float32 lr tensor with weight decay keeps the plan: the row carries the
     # weight decay for which the kernels' double factor is torch's float32 one
     from gefen_amd.gefen import _kernel_weight_decay
