@@ -262,7 +262,7 @@ def step_bytes(opt, params):
     return total
 
 
-STEP_KERNEL_SOURCES = ("gefen_amd/csrc/step.hip", "gefen_amd/csrc/common.h")
+STEP_KERNEL_SOURCES = ("gefen_amd/csrc/step_kernels.h", "gefen_amd/csrc/common.h")
 
 
 def step_kernel_sources_sha256():
