@@ -230,6 +230,50 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t v, int width) {
     return v;
 }
 
+// v of lane (this lane ^ OFF) in a wave whose 64 lanes are all active, without
+// lane-address arithmetic on the vector ALU: DPP quad permutations for 1 and 2,
+// DPP rotation by 8 inside each row of 16 lanes for 8 (i + 8 mod 16 == i ^ 8),
+// ds_swizzle (bitmask mode: source lane = lane ^ OFF inside 32 lanes) for 4 and
+// 16, ds_bpermute for 32.
+template <int OFF>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    if constexpr (OFF == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (OFF == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (OFF == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+    } else if constexpr (OFF == 4 || OFF == 16) {
+        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (OFF << 10) | 0x1f);
+    } else {
+        static_assert(OFF == 32, "lane_xor: offsets 1, 2, 4, 8, 16, 32");
+        return (uint32_t)__builtin_amdgcn_ds_bpermute((int)(((threadIdx.x & 63u) ^ 32u) << 2), (int)v);
+    }
+}
+
+// The butterflies of group_max_u32 / group_sum (the same lane pairs, offsets
+// width/2 down to 1, the same operand order, so the same results) for a width
+// that is uniform across the wave and a wave with every lane active.
+__device__ __forceinline__ uint32_t wave_group_max_u32(uint32_t v, int width) {
+    auto mx = [](uint32_t a, uint32_t b) { return b > a ? b : a; };
+    if (width > 32) v = mx(v, lane_xor<32>(v));
+    if (width > 16) v = mx(v, lane_xor<16>(v));
+    if (width > 8) v = mx(v, lane_xor<8>(v));
+    if (width > 4) v = mx(v, lane_xor<4>(v));
+    if (width > 2) v = mx(v, lane_xor<2>(v));
+    if (width > 1) v = mx(v, lane_xor<1>(v));
+    return v;
+}
+__device__ __forceinline__ float wave_group_sum(float v, int width) {
+    if (width > 32) v = v + __uint_as_float(lane_xor<32>(__float_as_uint(v)));
+    if (width > 16) v = v + __uint_as_float(lane_xor<16>(__float_as_uint(v)));
+    if (width > 8) v = v + __uint_as_float(lane_xor<8>(__float_as_uint(v)));
+    if (width > 4) v = v + __uint_as_float(lane_xor<4>(__float_as_uint(v)));
+    if (width > 2) v = v + __uint_as_float(lane_xor<2>(__float_as_uint(v)));
+    if (width > 1) v = v + __uint_as_float(lane_xor<1>(__float_as_uint(v)));
+    return v;
+}
+
 // Nearest codebook index of x with at most two threshold probes in the common
 // case, from bucket8 (FINE: bucket_fine).  The bucket is taken one below
 // floor((x + 1) * cells / 2) so that the fma's rounding can only move it down;

@@ -489,11 +489,11 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
             }
             if (!P1) sumsq = sumsq + ((lir + j * lpr < T.nvec) ? sj : 0.0f);
         }
-        const float mx = __uint_as_float(group_max_u32(mxk, lpr));
+        const float mx = __uint_as_float(wave_group_max_u32(mxk, lpr));
         float ss = 0.0f;
         if (!P1) {
             if (T.mode == kVmeanUpdate) {
-                const float tot = group_sum(sumsq, lpr);
+                const float tot = wave_group_sum(sumsq, lpr);
                 const float ms = tot / (float)T.period;
                 const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, rowv * T.b2));
                 if (active && lir == 0) vm[rsub] = vnew;
@@ -818,7 +818,7 @@ __global__ __launch_bounds__(kThreads) void k_muon(const MuonBatch B) {
                 }
             }
         }
-        const float mx = __uint_as_float(group_max_u32(mxk, lpr));
+        const float mx = __uint_as_float(wave_group_max_u32(mxk, lpr));
         const S mag_s = from_f32<S>(mx);
         if (active && lir == 0) mag[rsub] = mag_s;
         const float ms = to_f32(mag_s);
