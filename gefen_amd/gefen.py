@@ -20,6 +20,7 @@ device.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from itertools import chain
 from pathlib import Path
@@ -267,6 +268,30 @@ def _stream_handle(index: int) -> int:
     if _raw_stream is not None:
         return _raw_stream(index)
     return torch.cuda.current_stream(index).cuda_stream
+
+
+def _step_entry(impl):
+    """Optimizer.step of the Gefen optimizers.  torch.optim.Optimizer wraps a
+    subclass's step in profile_hook_step: a record_function range around the step
+    pre-hooks, the step and the post-hooks.  This entry runs that same wrapper
+    whenever a step hook is registered (on the optimizer or globally) or a
+    profiler is running, and the step alone otherwise, which keeps the
+    record_function dispatch off every step's host path.  ``hooked`` tells
+    Optimizer.__init__ not to wrap it again."""
+    from torch.optim import optimizer as _optim
+
+    hooked = torch.optim.Optimizer.profile_hook_step(impl)
+
+    @functools.wraps(impl)
+    def step(self, *args, **kwargs):
+        if (self._optimizer_step_pre_hooks or self._optimizer_step_post_hooks
+                or _optim._global_optimizer_pre_hooks or _optim._global_optimizer_post_hooks
+                or torch._C._autograd._profiler_enabled()):
+            return hooked(self, *args, **kwargs)
+        return impl(self, *args, **kwargs)
+
+    step.hooked = True
+    return step
 
 
 def _local(tensor):
@@ -1010,17 +1035,50 @@ class Gefen(torch.optim.Optimizer):
                 device = cur.device if torch.is_tensor(cur) else param.device
                 live[key] = value.to(device=device, dtype=value.dtype)
 
-    @torch.no_grad()
+    @_step_entry
     def step(self, closure=None):
-        """gefen.py:1399-1420."""
-        self._maybe_refresh_gefen_codebook()
-        self._maybe_save_gefen_grad_histogram()
-        loss = None
-        if closure is not None:
-            with torch.enable_grad():
-                loss = closure()
-        self._step_all()
+        """gefen.py:1399-1420 (the reference's step runs under torch.no_grad(); here
+        the steady-state step through the cached plan records no autograd ops and
+        skips entering it)."""
+        if closure is None and self._plan is not None and self._cached_step():
+            return None
+        with torch.no_grad():
+            self._maybe_refresh_gefen_codebook()
+            self._maybe_save_gefen_grad_histogram()
+            loss = None
+            if closure is not None:
+                with torch.enable_grad():
+                    loss = closure()
+            self._step_all()
+            self._gefen_global_step += 1
+            if self._exit_after_grad_sq_save:
+                raise SystemExit(0)
+            return loss
+
+    def _cached_step(self) -> bool:
+        """step() without a closure through the cached plan: taken when the codebook
+        is in place on the gradients' device and no gradient-histogram save is due
+        this step (the two checks at the top of step() then do nothing).  The kept
+        launches write the tensors through their device addresses, so no autograd
+        op is recorded.  False, with nothing changed, when the plan no longer
+        applies; step() then runs in full."""
+        cb = self._gefen_codebook
+        if cb is None or cb.device != self._gefen_codebook_device():
+            return False
+        due = getattr(quantization_module, "LIST_STEPS_SAVE_HIST_GRAD", None)
+        if due is not None and self._gefen_global_step in due:
+            return False
+        plan = self._plan
+        tables = self._codebook_tables()
+        if torch.cuda.current_device() == plan.dev_index:
+            done = plan.step(self, tables, _stream_handle(plan.dev_index))
+        else:
+            with torch.cuda.device(plan.device):
+                done = plan.step(self, tables, _stream_handle(plan.dev_index))
+        if not done:
+            self._plan = None
+            return False
         self._gefen_global_step += 1
         if self._exit_after_grad_sq_save:
             raise SystemExit(0)
-        return loss
+        return True

@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 
 from gefen_amd import _lib
-from gefen_amd.gefen import (Gefen, _DTYPE_CODE, _distinct, _gefen_host, _plan_checks_python,
+from gefen_amd.gefen import (Gefen, _DTYPE_CODE, _distinct, _gefen_host, _plan_checks_python, _step_entry,
                              _kernel_weight_decay, automatic_partition_view)
 
 EPS = 1e-7
@@ -283,6 +283,7 @@ class GefenMuon(Gefen):
                                                                  for key, idx in stacks.items()], dev, sumsq)
         del keep
 
+    @_step_entry
     @torch.no_grad()
     def step(self, closure=None):
         """gefen_muon.py:331-350: closure first, then the codebook refresh."""

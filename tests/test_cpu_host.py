@@ -314,3 +314,73 @@ def test_kernel_weight_decay_reproduces_torch_float32_factor():
     assert _kernel_weight_decay(torch.tensor(0.5, dtype=torch.float32), 2.0) is None  # factor 0
     assert _kernel_weight_decay(torch.tensor(1e-3, dtype=torch.float64), 0.1) == 0.1
     assert _kernel_weight_decay(1e-3, 0.1) == 0.1 and _kernel_weight_decay(torch.tensor(1e-3), 0.0) == 0.0
+
+
+def _entry_optimizers():
+    """An optimizer whose step goes through gefen.py's _step_entry and one that
+    torch wraps itself (profile_hook_step), both logging their calls."""
+    from gefen_amd.gefen import _step_entry
+
+    def body(self, closure=None):
+        self.log.append(("step", closure))
+        return "loss"
+
+    class Entry(torch.optim.Optimizer):
+        def __init__(self, params):
+            super().__init__(params, {})
+            self.log = []
+
+        step = _step_entry(body)
+
+    class Torch(torch.optim.Optimizer):
+        def __init__(self, params):
+            super().__init__(params, {})
+            self.log = []
+
+        def step(self, closure=None):
+            return body(self, closure)
+
+    return Entry([torch.nn.Parameter(torch.zeros(2))]), Torch([torch.nn.Parameter(torch.zeros(2))])
+
+
+def test_step_entry_calls_hooks_and_profiler_range_as_torch_does():
+    """The Gefen optimizers' step entry (gefen.py: _step_entry) keeps
+    torch.optim.Optimizer's step contract: instance and global pre/post hooks in
+    torch's order, a pre-hook may replace the arguments, and a profiler sees the
+    'Optimizer.step#<class>.step' range; with no hook and no profiler the step
+    runs alone (torch's wrapper, which also calls _optimizer_step_code, is not
+    entered)."""
+    from torch.optim import optimizer as optim
+
+    entry, ref = _entry_optimizers()
+    assert type(entry).step.hooked
+    for opt in (entry, ref):
+        opt.code_calls = 0
+
+        def code(opt=opt):
+            opt.code_calls += 1
+
+        opt._optimizer_step_code = code
+    assert entry.step() == "loss" and entry.code_calls == 0
+    assert ref.step() == "loss" and ref.code_calls == 1
+    logs = []
+    for opt in (entry, ref):
+        log = []
+        hs = [opt.register_step_pre_hook(lambda o, a, k, log=log: log.append("pre")),
+              opt.register_step_post_hook(lambda o, a, k, log=log: log.append("post")),
+              opt.register_step_pre_hook(lambda o, a, k: ((a[0], "replaced"), {})),
+              optim.register_optimizer_step_pre_hook(lambda o, a, k, log=log: log.append("global pre")),
+              optim.register_optimizer_step_post_hook(lambda o, a, k, log=log: log.append("global post"))]
+        try:
+            assert opt.step() == "loss"
+        finally:
+            for h in hs:
+                h.remove()
+        logs.append((log, opt.log[-1]))
+    assert logs[0] == logs[1] == (["global pre", "pre", "post", "global post"], ("step", "replaced"))
+    assert entry.code_calls == 1
+    assert entry.step() == "loss" and entry.code_calls == 1  # hooks removed: the step alone again
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        entry.step()
+    assert "Optimizer.step#Entry.step" in [e.name for e in prof.events()]
+    assert entry.code_calls == 2

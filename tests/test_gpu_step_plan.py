@@ -175,3 +175,38 @@ def test_stream_handle_is_the_current_stream():
     with torch.cuda.stream(s):
         assert _stream_handle(0) == s.cuda_stream == torch.cuda.current_stream().cuda_stream
     assert _stream_handle(0) == torch.cuda.current_stream(0).cuda_stream
+
+
+def test_optimizer_step_with_and_without_step_hooks_agree():
+    """Gefen.step through the cached plan, with torch's step pre/post hooks
+    registered (the hooked entry) and without (the step alone): the same
+    parameters and state bit for bit, the hooks called once per step, the plan
+    kept in both."""
+    from gefen_amd.gefen import Gefen
+
+    def run(hooks):
+        g = torch.Generator().manual_seed(3)
+        ps = [torch.nn.Parameter((torch.randn(s, generator=g) * 0.02).to(torch.bfloat16).cuda())
+              for s in [(64, 256), (512,), (96, 128)]]
+        opt = Gefen([("p{}".format(i), p) for i, p in enumerate(ps)])
+        calls = []
+        if hooks:
+            opt.register_step_pre_hook(lambda o, a, k: calls.append("pre"))
+            opt.register_step_post_hook(lambda o, a, k: calls.append("post"))
+        for step in range(4):
+            gg = torch.Generator().manual_seed(10 + step)
+            for p in ps:
+                p.grad = (torch.randn(p.shape, generator=gg) * 1e-3).to(torch.bfloat16).cuda()
+            opt.step()
+        torch.cuda.synchronize()
+        return ps, opt, calls
+
+    a, oa, ca = run(False)
+    b, ob, cb = run(True)
+    assert ca == [] and cb == ["pre", "post"] * 4
+    assert oa._plan is not None and ob._plan is not None
+    assert oa._gefen_global_step == ob._gefen_global_step == 4
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+        for k in ("m_codebook", "m_magnitude", "vmean"):
+            assert torch.equal(oa.state[x][k], ob.state[y][k]), k
