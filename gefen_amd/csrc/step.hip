@@ -419,6 +419,8 @@ void plan_luts(const std::vector<PendingStep>& pend, LutPlan& lp) {
         const Key& k = pend[i].key;
         if (!k.p1 || k.s == GEFEN_F32) continue;
         const StepTask& t = pend[i].task;
+        // bf16 states outside the square-root table's bounds compute every stepsize
+        if (k.s == GEFEN_BF16 && !root_table_ok(t.sqrt_bc2, t.eps)) continue;
         int found = -1;
         for (size_t j = 0; j < lp.keys.size(); ++j)
             if (lp.keys[j].s == k.s && memcmp(&lp.keys[j].a, &t.sqrt_bc2, 4) == 0 &&

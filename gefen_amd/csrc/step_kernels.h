@@ -204,6 +204,14 @@ __device__ __forceinline__ int find_task(const int32_t* wg_begin, int ntasks) {
     return lo;
 }
 
+// sum / n rounded once (the block mean of g^2, gefen.py:116-117): a power-of-two
+// n (uniform) divides exactly by multiplying with 2^-log2(n), which rounds the
+// same real number; other n take the IEEE division.
+__device__ __forceinline__ float mean_of(float sum, int32_t n) {
+    if ((n & (n - 1)) == 0) return sum * __int_as_float((127 - __builtin_ctz((uint32_t)n)) << 23);
+    return sum / (float)n;
+}
+
 // stepsize of gefen.py:1326-1327: (1/bc1) * reciprocal(sqrt(v)/sqrt(bc2) + eps)
 __device__ __forceinline__ float stepsize_of(float v, const StepTask& T) {
     float h = sqrtf(v) / T.sqrt_bc2 + T.eps;
@@ -228,28 +236,33 @@ __device__ __forceinline__ float p1_stepsize(S v, const StepTask& T) {
 // table root.  A finite v >= 0 is M * 2^E with an integer M < 256 (128 +
 // mantissa for normal v, the mantissa for subnormal v), E = max(exponent
 // field, 1) - 134.  With par = E mod 2 and half = floor(E / 2) = (bits >> 8) - 67,
-// sqrt(v) = sqrt(M * 2^par) * 2^half, and since every value here is a normal
-// float (sqrt(v) >= 2^-67, sqrt(bc2) >= 2^-27), scaling by powers of two
-// commutes with rounding:
+// sqrt(v) = sqrt(M * 2^par) * 2^half.  A launch reads the table only when
+// 2^-60 <= sqrt_bc2 <= 2^30 and 2^-126 <= eps <= 2^100 (root_table_ok), so
+// every value here is a normal float (2^-67 <= sqrt(v) < 2^64 and 2^-97 <=
+// fl(sqrt(v)) / sqrt_bc2 <= 2^124 for v > 0, nonzero table entries in
+// [2^-97, 2^-2]) and scaling by powers of two commutes with rounding:
 //   fl(fl(sqrt(v)) / sqrt_bc2) = root[i] * 2^(bits >> 8)   exactly, with
 //   i = bits & 0xff   for normal v (= par * 128 + mantissa; E and the exponent
 //                     field have the same parity),
 //   i = 256 + bits    for subnormal v and zero (par = 1),
 //   root[i] = fl(fl(sqrt(M * 2^par)) / sqrt_bc2) * 2^-67   (k_build_root).
-// root_h returns h = that + eps.
+// root_h returns h = that + eps, in [2^-126, 2^126) by the same bounds (eps for
+// v = 0, at least 2^-97 for v > 0, at most 2^124 + 2^100).
 __device__ __forceinline__ float root_h(uint32_t bits, const StepTask& T, const float* root) {
     const uint32_t i = bits < 0x80u ? bits + 256u : (bits & 0xffu);
     return __builtin_ldexpf(root[i], (int)(bits >> 8)) + T.eps;
 }
 
-// root_h and the reciprocal are exact where this holds: v finite and >= 0
-// (bits < 0x7f80) and 2^-126 <= h < 2^126.  In that range the reciprocal
-// fma(fma(-h, r, 1), r, r) with r = v_rcp_f32(h) equals the IEEE quotient 1 / h
-// (checked on gfx950 for every float h in the range); other values take
-// stepsize_of.
-__device__ __forceinline__ bool root_ok(uint32_t bits, float h) {
-    return bits < 0x7f80u && __float_as_uint(h) - 0x00800000u < 0x7e000000u;
+// The bounds of root_h on the table's settings (checked on the host per launch).
+__host__ __device__ inline bool root_table_ok(float sqrt_bc2, float eps) {
+    return sqrt_bc2 >= 0x1p-60f && sqrt_bc2 <= 0x1p30f && eps >= 0x1p-126f && eps <= 0x1p100f;
 }
+
+// root_h is exact for finite v >= 0 (bits < 0x7f80); negative, inf and NaN
+// states take stepsize_of.  In root_h's range of h the reciprocal
+// fma(fma(-h, r, 1), r, r) with r = v_rcp_f32(h) equals the IEEE quotient 1 / h
+// (checked on gfx950 for every float h in [2^-126, 2^126)).
+__device__ __forceinline__ bool root_ok(uint32_t bits) { return bits < 0x7f80u; }
 
 __device__ __forceinline__ float root_stepsize(float h, const StepTask& T) {
     const float r = __builtin_amdgcn_rcpf(h);
@@ -317,9 +330,8 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables<F
                 vo.v[w] = vnew;
                 if constexpr (std::is_same<S, bf16_t>::value) {
                     if (root) {
-                        const float h = root_h(vnew.bits, T, root);
-                        special = special || !root_ok(vnew.bits, h);
-                        sw[w] = root_stepsize(h, T);
+                        special = special || !root_ok(vnew.bits);
+                        sw[w] = root_stepsize(root_h(vnew.bits, T, root), T);
                     } else {
                         sw[w] = stepsize_of(to_f32(vnew), T);
                     }
@@ -331,7 +343,7 @@ __device__ __forceinline__ void step_sweep2(const StepTask& T, const LdsTables<F
                 if (special) {  // one branch per vector for the rare values outside the table's range
 #pragma unroll
                     for (int w = 0; w < W; ++w)
-                        if (!root_ok(vo.v[w].bits, root_h(vo.v[w].bits, T, root)))
+                        if (!root_ok(vo.v[w].bits))
                             sw[w] = stepsize_of(to_f32(vo.v[w]), T);
                 }
             }
@@ -494,7 +506,7 @@ __global__ __launch_bounds__(kStepThreads) void k_gefen_step(const StepBatch B) 
         if (!P1) {
             if (T.mode == kVmeanUpdate) {
                 const float tot = wave_group_sum(sumsq, lpr);
-                const float ms = tot / (float)T.period;
+                const float ms = mean_of(tot, T.period);
                 const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, rowv * T.b2));
                 if (active && lir == 0) vm[rsub] = vnew;
                 ss = stepsize_of(to_f32(vnew), T);
@@ -586,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void k_gefen_step_long(const StepBatch B)
     const float tot = (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
     float ss;
     if (T.mode == kVmeanUpdate) {
-        const float ms = tot / (float)T.period;
+        const float ms = mean_of(tot, T.period);
         const float prev = to_f32(vm[row]) * T.b2;
         const S vnew = from_f32<S>(__builtin_fmaf(ms, T.omb2, prev));
         ss = stepsize_of(to_f32(vnew), T);

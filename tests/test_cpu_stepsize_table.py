@@ -1,7 +1,10 @@
 """The period-one stepsize of a bf16 state through a 384-entry square-root table
-(csrc/step.hip: k_build_root, root_h, root_ok, root_stepsize) equals the direct
-float32 expression of gefen.py:1326-1327, h = sqrt(v) / sqrt(bc2) + eps,
-stepsize = (1 / bc1) / h, for every bf16 bit pattern (NaN for NaN).
+(csrc/step_kernels.h: root_h, root_ok, root_table_ok, root_stepsize;
+csrc/step.hip: k_build_root) equals the direct float32 expression of
+gefen.py:1326-1327, h = sqrt(v) / sqrt(bc2) + eps, stepsize = (1 / bc1) / h,
+for every bf16 bit pattern (NaN for NaN), at every setting the host lets a
+launch read the table (root_table_ok), and h stays inside the reciprocal's
+range [2^-126, 2^126) there.
 
 numpy's float32 sqrt, division and addition are correctly rounded and ldexp is
 exact on normal results, so this checks the identity the kernel relies on,
@@ -32,18 +35,23 @@ def _root_table(c):
     return root
 
 
+def _root_table_ok(c, eps):
+    """root_table_ok: the settings at which a launch reads the table."""
+    return bool(2.0 ** -60 <= c <= 2.0 ** 30 and 2.0 ** -126 <= eps <= 2.0 ** 100)
+
+
 def _table(bits, c, eps, inv_bc1):
-    """root_h, root_ok, root_stepsize (IEEE reciprocal), and stepsize_of where root_ok fails."""
+    """root_h, root_ok, root_stepsize (IEEE reciprocal), and stepsize_of where root_ok
+    fails or the setting is outside root_table_ok; also h and where the table applied."""
     root = _root_table(c)
     i = np.where(bits < 0x80, bits + 256, bits & 0xFF)
     scaled = np.ldexp(root[i], (bits >> 8).astype(np.int32))
     assert scaled.dtype == F32
     h = scaled + eps
-    hb = h.view(np.uint32).astype(np.int64)
-    ok = (bits < 0x7F80) & ((hb - 0x00800000) % (1 << 32) < 0x7E000000)
+    ok = (bits < 0x7F80) & _root_table_ok(c, eps)
     table = (F32(1.0) / h) * inv_bc1
     v = (bits << 16).view(F32)
-    return np.where(ok, table, _direct(v, c, eps, inv_bc1)), ok
+    return np.where(ok, table, _direct(v, c, eps, inv_bc1)), ok, h
 
 
 @pytest.mark.parametrize("beta2,step,eps", [
@@ -58,8 +66,10 @@ def test_square_root_table_matches_the_direct_expression(beta2, step, eps):
     c, eps_f, inv_bc1 = F32(np.sqrt(bc2)), F32(eps), F32(1.0 / bc1)
     with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
         want = _direct(v, c, eps_f, inv_bc1)
-        got, ok = _table(bits, c, eps_f, inv_bc1)
+        got, ok, h = _table(bits, c, eps_f, inv_bc1)
     assert ok[bits < 0x7F80].all()  # every finite v >= 0 takes the table at these settings
+    hb = h[bits < 0x7F80].view(np.uint32)
+    assert ((hb >= 0x00800000) & (hb < 0x7E800000)).all()  # h in [2^-126, 2^126): the exact reciprocal
     nan = np.isnan(want)
     assert np.isfinite(want[bits < 0x7F80]).all()
     assert nan.sum() == (bits > 0x8000).sum() + 127  # every v < 0 but -0, and the 127 positive NaNs
@@ -70,9 +80,30 @@ def test_square_root_table_matches_the_direct_expression(beta2, step, eps):
 def test_values_outside_the_table_range_take_the_direct_path():
     bits = np.array([0x0000, 0x7F80, 0x8000, 0x8001, 0xFF80, 0x7FC0], dtype=np.uint32)
     with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
-        got, ok = _table(bits, F32(1.0), F32(0.0), F32(1.0))  # eps = 0: h = 0 for v = 0
+        got, ok, _ = _table(bits, F32(1.0), F32(0.0), F32(1.0))  # eps = 0: no table (h = 0 for v = 0)
     np.testing.assert_array_equal(ok, [False, False, False, False, False, False])
     assert got[0] == np.inf and got[1] == 0.0 and np.isinf(got[2]) and np.isnan(got[3:]).all()
+    got, ok, _ = _table(bits, F32(1.0), F32(1e-8), F32(1.0))  # in bounds: only finite v >= 0
+    np.testing.assert_array_equal(ok, [True, False, False, False, False, False])
+
+
+@pytest.mark.parametrize("c,eps", [(2.0 ** -60, 2.0 ** -126), (2.0 ** 30, 2.0 ** -126), (2.0 ** -60, 2.0 ** 100),
+                                   (2.0 ** 30, 2.0 ** 100)])
+def test_table_bounds_keep_h_in_the_reciprocal_range(c, eps):
+    """At the corners of root_table_ok the table still equals the direct
+    expression and h stays in [2^-126, 2^126) for every finite v >= 0."""
+    bits = np.arange(0x7F80, dtype=np.uint32)
+    v = (bits << 16).view(F32)
+    assert _root_table_ok(c, eps)
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        want = _direct(v, F32(c), F32(eps), F32(1.0))
+        got, ok, h = _table(bits, F32(c), F32(eps), F32(1.0))
+    assert ok.all()
+    hb = h.view(np.uint32)
+    assert ((hb >= 0x00800000) & (hb < 0x7E800000)).all()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert not _root_table_ok(c * 2.0 if c > 1 else c / 2.0, eps)
+    assert not _root_table_ok(c, eps * 2.0 if eps > 1 else eps / 2.0)
 
 
 def test_table_index_covers_subnormals_zero_and_both_exponent_parities():
