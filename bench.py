@@ -596,16 +596,29 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
         if plan is None or not plan.handle:
             raise RuntimeError("the optimizer did not keep a step plan")
         _lib.check(lib.gefen_step_plan_time_runs(plan.handle, 1))
-        in_step = []
+        in_step, host, outside = [], [], []
+        cur = torch.cuda.current_stream()
         for _ in range(args.steps):
             set_grads(step_no)
             step_no += 1
+            # also: the host time of the step() call, and the GPU time between an
+            # event recorded right before the call and one recorded right after it
+            # that the step's launches do not cover (the host's work before the
+            # first launch reaches the GPU, and the join of the side stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cur)
+            t0 = time.perf_counter()
             opt.step()
+            t1 = time.perf_counter()
+            e1.record(cur)
             if opt._plan is not plan:
                 raise RuntimeError("the step plan was rebuilt during the timed steps")
+            torch.cuda.synchronize()
             ms = ctypes.c_float()
             _lib.check(lib.gefen_step_plan_last_ms(plan.handle, ctypes.byref(ms)))
             in_step.append(ms.value)
+            host.append((t1 - t0) * 1000.0)
+            outside.append(e0.elapsed_time(e1) - ms.value)
         _lib.check(lib.gefen_step_plan_time_runs(plan.handle, 0))
         kms = statistics.median(in_step)
         # the same launches back to back on unchanged gradients (the kernels' own
@@ -633,7 +646,9 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
                            "step_frac": round(nbytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                            "kernel_ms_back_to_back": round(kms_b2b, 4),
                            "frac_back_to_back": round(nbytes / (kms_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                           "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
+                           "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4),
+                           "host_ms_per_step": round(statistics.median(host), 4),
+                           "gpu_ms_outside_launches": round(statistics.median(outside), 4)}
         if with_cpu:
             out["cpu_baseline"] = cpu_baseline(opt, params, budget_s=cpu_budget_s)
     else:
@@ -647,7 +662,7 @@ def compact(out):
     """The figures of a further config's line that the headline line carries."""
     r = out["roofline"]
     keep = ("bound", "achieved", "peak", "unit", "frac", "kernel_ms_per_step", "step_frac", "frac_back_to_back",
-            "frac_of_copy")
+            "frac_of_copy", "host_ms_per_step", "gpu_ms_outside_launches")
     return {"workload": out["config"]["workload"], "ms_per_step": out["value"], "p10_ms": out["p10_ms"],
             "p90_ms": out["p90_ms"], "first_step_ms": out["first_step_ms"], "dtype": out["dtype"],
             "vs_readme": out["vs_baseline"], "periods": out["config"]["periods"],
