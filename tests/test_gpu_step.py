@@ -72,11 +72,15 @@ def test_step_tasks_match_oracle(case):
 
 # Period-one bf16 states over the whole bf16 range: per-row gradient scales from
 # 2^-66 to 2^18 put the new vmean on subnormals, zero, every exponent in between
-# and large values, each read through the kernel's square-root table.
+# and large values, each read through the kernel's square-root table; eps = 0 and
+# eps = 2^101 lie outside the settings whose launches read the table
+# (root_table_ok: 2^-126 <= eps <= 2^100), so those steps compute every stepsize.
 WIDE_CASES = [
     ("bf16_P1_wide_b2_half", 256 * 96, 0.5, 1e-8, -66, 18),
     ("bf16_P1_wide_eps_small", 256 * 96, 0.999, 1e-12, -66, 18),
     ("bf16_P1_wide_eps_large", 64 * 75, 0.9, 1e-3, -40, 10),
+    ("bf16_P1_wide_eps_zero_no_table", 256 * 96, 0.999, 0.0, -66, 18),
+    ("bf16_P1_wide_eps_huge_no_table", 64 * 75, 0.999, 2.0 ** 101, -40, 10),
 ]
 
 
