@@ -393,12 +393,30 @@ __global__ __launch_bounds__(kDpThreads) void k_dp_level(int c, int K, int force
     }
     const int cnt = N - c + 1;  // ends c .. N
     if (blockIdx.x > 0 && 2 * (int)blockIdx.x * kDpWaves >= cnt) return;  // no pair of ends here (uniform)
-    // indices c - 1 .. N of the four arrays (s - 1 >= c - 1, e <= N)
-    for (int i = c - 1 + (int)threadIdx.x; i <= N; i += kDpThreads) {
-        spw[i] = pw[i];
-        spwx[i] = pwx[i];
-        spwx2[i] = pwx2[i];
-        sprev[i] = prev[i];
+    // indices c - 1 .. N of the four arrays (s - 1 >= c - 1, e <= N); every load of
+    // a thread is issued before its first LDS store, so the staging waits for one
+    // round trip to L2 instead of one per pass
+    constexpr int kStage = (kDpMaxBins + 1 + kDpThreads - 1) / kDpThreads;
+    double st[4][kStage];
+#pragma unroll
+    for (int r = 0; r < kStage; ++r) {
+        const int i = c - 1 + (int)threadIdx.x + r * kDpThreads;
+        if (i <= N) {
+            st[0][r] = pw[i];
+            st[1][r] = pwx[i];
+            st[2][r] = pwx2[i];
+            st[3][r] = prev[i];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kStage; ++r) {
+        const int i = c - 1 + (int)threadIdx.x + r * kDpThreads;
+        if (i <= N) {
+            spw[i] = st[0][r];
+            spwx[i] = st[1][r];
+            spwx2[i] = st[2][r];
+            sprev[i] = st[3][r];
+        }
     }
     __syncthreads();
     const int lane = threadIdx.x & 63;
