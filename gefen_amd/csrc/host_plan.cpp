@@ -196,6 +196,9 @@ class PlanCore {
         int64_t* steps = reinterpret_cast<int64_t*>(steps_out);
         double last_b1 = 0.0, last_b2 = 0.0, bc1 = 0.0, bc2 = 0.0;
         long long last_step = -1;
+        // one int object per distinct step count, shared by the state dicts that take it
+        py::object step_obj;
+        long long step_obj_val = -1;
         for (k = 0; k < n; ++k) {
             char* row = reinterpret_cast<char*>(table + k * stride);
             const uint64_t gp = gptr_[k];
@@ -213,10 +216,13 @@ class PlanCore {
                 std::memcpy(row + col[6], &bc1, 8);
                 std::memcpy(row + col[7], &bc2, 8);
             }
-            PyObject* v = PyLong_FromLongLong(step_[k]);
-            if (!v) throw py::error_already_set();
-            const int rc = PyDict_SetItem(states_[k].ptr(), key_step_, v);
-            Py_DECREF(v);
+            if (!step_obj || step_obj_val != step_[k]) {
+                PyObject* v = PyLong_FromLongLong(step_[k]);
+                if (!v) throw py::error_already_set();
+                step_obj = py::reinterpret_steal<py::object>(v);
+                step_obj_val = step_[k];
+            }
+            const int rc = PyDict_SetItem(states_[k].ptr(), key_step_, step_obj.ptr());
             sver_[k] = rc == 0 ? dict_version(states_[k].ptr()) : 0;
             committed_[k] = step_[k];
             if (rc != 0) throw py::error_already_set();
