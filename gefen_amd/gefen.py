@@ -281,12 +281,17 @@ def _step_entry(impl):
     from torch.optim import optimizer as _optim
 
     hooked = torch.optim.Optimizer.profile_hook_step(impl)
+    # without torch's profiler query (or its global hook tables) every step takes the wrapper
+    profiling = getattr(getattr(torch._C, "_autograd", None), "_profiler_enabled", None)
+    pre = getattr(_optim, "_global_optimizer_pre_hooks", None)
+    post = getattr(_optim, "_global_optimizer_post_hooks", None)
+    if profiling is None or pre is None or post is None:
+        hooked.hooked = True
+        return hooked
 
     @functools.wraps(impl)
     def step(self, *args, **kwargs):
-        if (self._optimizer_step_pre_hooks or self._optimizer_step_post_hooks
-                or _optim._global_optimizer_pre_hooks or _optim._global_optimizer_post_hooks
-                or torch._C._autograd._profiler_enabled()):
+        if (self._optimizer_step_pre_hooks or self._optimizer_step_post_hooks or pre or post or profiling()):
             return hooked(self, *args, **kwargs)
         return impl(self, *args, **kwargs)
 
