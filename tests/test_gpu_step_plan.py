@@ -210,3 +210,54 @@ def test_optimizer_step_with_and_without_step_hooks_agree():
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
         for k in ("m_codebook", "m_magnitude", "vmean"):
             assert torch.equal(oa.state[x][k], ob.state[y][k]), k
+
+
+@pytest.mark.parametrize("opt_name", ["Gefen", "GefenMuon"])
+def test_step_with_closure_returns_its_loss_and_equals_a_manual_backward(opt_name):
+    """step(closure) (gefen.py:1399-1420, gefen_muon.py:331-350): the closure runs with
+    gradients enabled even when the caller's mode is no_grad, step returns its loss,
+    the caller's grad mode is unchanged afterwards, and the parameters equal a run
+    that calls backward before a plain step(), bit for bit, over three steps (the
+    later ones through the cached plan).  Gefen refreshes its codebook before it runs
+    the closure, as the reference does, so its first step needs gradients already
+    present (the first step of both runs is a plain one there); GefenMuon runs the
+    closure first."""
+    from gefen_amd import Gefen, GefenMuon
+
+    cls = {"Gefen": Gefen, "GefenMuon": GefenMuon}[opt_name]
+
+    def make():
+        g = torch.Generator().manual_seed(11)
+        w = torch.nn.Parameter((torch.randn(128, 256, generator=g) * 0.02).cuda())
+        x = torch.randn(16, 256, generator=g).cuda()
+        return w, x
+
+    w1, x = make()
+    w2, _ = make()
+    o1, o2 = cls([("w", w1)]), cls([("w", w2)])
+    for step in range(3):
+        if step == 0 and opt_name == "Gefen":
+            for w, o in ((w1, o1), (w2, o2)):
+                o.zero_grad()
+                (x @ w.t()).pow(2).mean().backward()
+                o.step()
+            continue
+
+        def closure():
+            assert torch.is_grad_enabled()
+            o1.zero_grad()
+            loss = (x @ w1.t()).pow(2).mean()
+            loss.backward()
+            return loss
+
+        with torch.no_grad():
+            loss1 = o1.step(closure)
+            assert not torch.is_grad_enabled()
+        o2.zero_grad()
+        loss2 = (x @ w2.t()).pow(2).mean()
+        loss2.backward()
+        assert o2.step() is None
+        torch.cuda.synchronize()
+        assert torch.equal(loss1, loss2)
+        assert torch.equal(w1.detach(), w2.detach())
+    assert o1._gefen_global_step == o2._gefen_global_step == 3
