@@ -116,6 +116,38 @@ class PlanCore {
     // With cols = (grad,) only the gradient addresses and the step counts are
     // written (the caller handles the hyperparameters).
     bool refresh(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols, uintptr_t steps_out) {
+        if (!prepare(param_groups, table, stride, cols)) return false;
+        commit(steps_out);
+        return true;
+    }
+
+    // refresh(), then, when its checks passed, the step itself: run_fn is the
+    // address of the C ABI's gefen_step_plan_run, called with (plan, table, number
+    // of rows, stream) once the table rows are written, so a cached step costs one
+    // call from Python.  The state dicts' "step" entries and steps_out are written
+    // after the launches (they are not read before), which keeps those writes off
+    // the GPU's wait for the first launch.  Returns -1 when the plan no longer
+    // applies (nothing was changed or launched), else gefen_step_plan_run's status
+    // (the step counts advance in either case).
+    int step(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols, uintptr_t steps_out,
+             uintptr_t run_fn, uintptr_t plan, uintptr_t stream) {
+        if (!run_fn || !plan) throw py::value_error("PlanCore.step: null run function or plan");
+        if (!prepare(param_groups, table, stride, cols)) return -1;
+        using RunFn = int (*)(void*, const void*, int, void*);
+        const int rc = reinterpret_cast<RunFn>(run_fn)(reinterpret_cast<void*>(plan),
+                                                       reinterpret_cast<const void*>(table),
+                                                       static_cast<int>(params_.size()), reinterpret_cast<void*>(stream));
+        commit(steps_out);
+        return rc;
+    }
+
+    size_t size() const { return params_.size(); }
+
+   private:
+    // The checks of refresh() and the table rows: gradient addresses and, with
+    // hyperparameter columns, the hyperparameters and bias corrections of step + 1.
+    // A failed check (false) leaves the table and the state dicts as they were.
+    bool prepare(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols) {
         if (!PyList_Check(param_groups.ptr()) || (cols.size() != 8 && cols.size() != 1)) return false;
         const bool hyper = cols.size() == 8;
         size_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -192,13 +224,9 @@ class PlanCore {
             }
             step_[k] = v + 1;
         }
-        // every check passed: commit
-        int64_t* steps = reinterpret_cast<int64_t*>(steps_out);
+        // every check passed: the table rows
         double last_b1 = 0.0, last_b2 = 0.0, bc1 = 0.0, bc2 = 0.0;
         long long last_step = -1;
-        // one int object per distinct step count, shared by the state dicts that take it
-        py::object step_obj;
-        long long step_obj_val = -1;
         for (k = 0; k < n; ++k) {
             char* row = reinterpret_cast<char*>(table + k * stride);
             const uint64_t gp = gptr_[k];
@@ -216,6 +244,19 @@ class PlanCore {
                 std::memcpy(row + col[6], &bc1, 8);
                 std::memcpy(row + col[7], &bc2, 8);
             }
+        }
+        return true;
+    }
+
+    // The advanced step counts of the last successful prepare(): each state's
+    // "step" entry and steps_out (n int64 slots).
+    void commit(uintptr_t steps_out) {
+        int64_t* steps = reinterpret_cast<int64_t*>(steps_out);
+        // one int object per distinct step count, shared by the state dicts that take it
+        py::object step_obj;
+        long long step_obj_val = -1;
+        const size_t n = params_.size();
+        for (size_t k = 0; k < n; ++k) {
             if (!step_obj || step_obj_val != step_[k]) {
                 PyObject* v = PyLong_FromLongLong(step_[k]);
                 if (!v) throw py::error_already_set();
@@ -228,26 +269,8 @@ class PlanCore {
             if (rc != 0) throw py::error_already_set();
             steps[k] = step_[k];
         }
-        return true;
     }
 
-    // refresh(), then, when it succeeded, the step itself: run_fn is the address of
-    // the C ABI's gefen_step_plan_run, called with (plan, table, number of rows,
-    // stream) while the table is fresh, so a cached step costs one call from
-    // Python.  Returns -1 when the plan no longer applies (nothing was changed or
-    // launched), else gefen_step_plan_run's status.
-    int step(py::handle param_groups, uintptr_t table, int64_t stride, py::tuple cols, uintptr_t steps_out,
-             uintptr_t run_fn, uintptr_t plan, uintptr_t stream) {
-        if (!run_fn || !plan) throw py::value_error("PlanCore.step: null run function or plan");
-        if (!refresh(param_groups, table, stride, cols, steps_out)) return -1;
-        using RunFn = int (*)(void*, const void*, int, void*);
-        return reinterpret_cast<RunFn>(run_fn)(reinterpret_cast<void*>(plan), reinterpret_cast<const void*>(table),
-                                               static_cast<int>(params_.size()), reinterpret_cast<void*>(stream));
-    }
-
-    size_t size() const { return params_.size(); }
-
-   private:
     // lr (a number or a 0-d tensor), beta1, beta2, eps, weight_decay of a group,
     // the weight decay as the kernels take it.  For a float32 tensor lr with
     // weight decay, torch forms the decay factor in float32,
