@@ -22,7 +22,11 @@ written into the same gradient buffers (outside the timed region).
   ms_per_step (host time included).  frac_back_to_back: the launches repeated
   back to back on unchanged gradients.  copy_kernel_gbs: a plain 2 GiB device
   copy (16-byte vectors) timed on the same box, and frac_of_copy the step's
-  bandwidth as a fraction of it.
+  bandwidth as a fraction of it.  host_ms_per_step: host time of the
+  optimizer.step() call; host_ms_plan_run / host_ms_step_tasks: host time of
+  the one C call that launches a cached step (gefen_step_plan_run) and of
+  gefen_step_tasks, which plans every launch anew (medians over calls issued
+  back to back).
 * cpu_baseline: the CPU oracle (C restatement of the reference CPU path,
   OpenMP) on a bounded sample of the same tensors, scaled to a full step.
 * other_configs (default config only, unless --headline-only): the metric's
@@ -630,12 +634,27 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
             _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream))
         reps = max(args.steps, 5)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        host_tasks = []
         e0.record(stream)
         for _ in range(reps):
-            _lib.check(lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream))
+            t0 = time.perf_counter()
+            rc = lib.gefen_step_tasks(tasks.ctypes.data, len(params), tables.data_ptr(), stream.cuda_stream)
+            host_tasks.append((time.perf_counter() - t0) * 1000.0)
+            _lib.check(rc)
         e1.record(stream)
         torch.cuda.synchronize()
         kms_b2b = e0.elapsed_time(e1) / reps
+        # host time of the C call that launches a cached step (gefen_step_plan_run on
+        # the plan's table as the last step refreshed it), beside that of
+        # gefen_step_tasks above, which plans every launch anew: each call timed
+        # alone on the host, issued back to back
+        host_run = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            rc = lib.gefen_step_plan_run(plan.handle, plan.tptr, len(plan.tasks), stream.cuda_stream)
+            host_run.append((time.perf_counter() - t0) * 1000.0)
+            _lib.check(rc)
+        torch.cuda.synchronize()
         nbytes = step_bytes(opt, params)
         achieved = nbytes / (kms * 1e-3) / 1e9
         if copy_gbs is None:
@@ -648,7 +667,9 @@ def measure(name, args, dev, with_cpu, copy_gbs=None, cpu_budget_s=20.0):
                            "frac_back_to_back": round(nbytes / (kms_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                            "copy_kernel_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4),
                            "host_ms_per_step": round(statistics.median(host), 4),
-                           "gpu_ms_outside_launches": round(statistics.median(outside), 4)}
+                           "gpu_ms_outside_launches": round(statistics.median(outside), 4),
+                           "host_ms_plan_run": round(statistics.median(host_run), 4),
+                           "host_ms_step_tasks": round(statistics.median(host_tasks), 4)}
         if with_cpu:
             out["cpu_baseline"] = cpu_baseline(opt, params, budget_s=cpu_budget_s)
     else:
@@ -662,7 +683,7 @@ def compact(out):
     """The figures of a further config's line that the headline line carries."""
     r = out["roofline"]
     keep = ("bound", "achieved", "peak", "unit", "frac", "kernel_ms_per_step", "step_frac", "frac_back_to_back",
-            "frac_of_copy", "host_ms_per_step", "gpu_ms_outside_launches")
+            "frac_of_copy", "host_ms_per_step", "gpu_ms_outside_launches", "host_ms_plan_run", "host_ms_step_tasks")
     return {"workload": out["config"]["workload"], "ms_per_step": out["value"], "p10_ms": out["p10_ms"],
             "p90_ms": out["p90_ms"], "first_step_ms": out["first_step_ms"], "dtype": out["dtype"],
             "vs_readme": out["vs_baseline"], "periods": out["config"]["periods"],
