@@ -704,8 +704,8 @@ def main():
                     help="also copy 2 GiB once with k_copy16 (a kernel of known traffic for scaling HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the step shards by partition block, "
-              "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the step would shard by partition "
+              "block, with no communication between GPUs). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     if args.config == "kernels":
