@@ -283,6 +283,66 @@ def test_plan_core_checks_and_commits_only_when_the_plan_applies():
     assert np.float32(1.0 - table["lr"][2] * table["weight_decay"][2]) == (1 - lr32 * 0.1).item()
 
 
+def test_plan_core_step_runs_between_the_table_rows_and_the_step_counts():
+    """PlanCore.step (gefen_amd/csrc/host_plan.cpp) calls the run function once,
+    with (plan, table, rows, stream), after the table rows are written and before
+    the state dicts' "step" entries and steps_out advance; it returns the run's
+    status and advances the counts whatever that status; when a check fails it
+    returns -1 without calling the run or changing table or counts."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from gefen_amd import _gefen_host, _lib
+
+    ps = [torch.nn.Parameter(torch.zeros(n)) for n in (8, 4)]
+    for p in ps:
+        p.grad = torch.ones_like(p)
+    states = [{"step": 5, "m_codebook": torch.zeros(1), "m_magnitude": torch.zeros(1), "vmean": torch.zeros(1)}
+              for _ in ps]
+    core = _gefen_host.PlanCore(list(ps), states, ("m_codebook", "m_magnitude", "vmean"))
+    groups = [{"params": list(ps), "lr": 1e-3, "beta1": 0.9, "beta2": 0.999, "eps": 1e-8, "weight_decay": 0}]
+    table = np.zeros(2, dtype=_lib.STEP_TASK)
+    steps = np.zeros(2, dtype=np.int64)
+    cols = tuple(table.dtype.fields[c][1] for c in ("grad", "lr", "beta1", "beta2", "eps", "weight_decay",
+                                                     "bias_correction_1", "bias_correction_2"))
+    seen = []
+    status = [0]
+
+    @ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p)
+    def run(plan, tasks, n, stream):
+        seen.append((plan, tasks, n, stream, table["grad"].tolist(), table["bias_correction_1"].tolist(),
+                     [st["step"] for st in states], steps.tolist()))
+        return status[0]
+
+    run_fn = ctypes.cast(run, ctypes.c_void_p).value
+
+    def step(gr):
+        return core.step(gr, table.ctypes.data, table.itemsize, cols, steps.ctypes.data, run_fn, 0x1234, 0x5678)
+
+    assert step(groups) == 0
+    grads = [p.grad.data_ptr() for p in ps]
+    assert seen == [(0x1234, table.ctypes.data, 2, 0x5678, grads, [1 - 0.9 ** 6] * 2, [5, 5], [0, 0])]
+    assert [st["step"] for st in states] == [6, 6] and steps.tolist() == [6, 6]
+    # a failed run still advances the counts (its launches may have started)
+    status[0] = 7
+    assert step(groups) == 7
+    assert seen[-1][6] == [6, 6] and [st["step"] for st in states] == [7, 7] and steps.tolist() == [7, 7]
+    # a failed check: no run, nothing written
+    g1 = ps[1].grad
+    ps[1].grad = torch.ones(8)[::2]  # not contiguous
+    table["grad"] = 0
+    assert step(groups) == -1
+    assert len(seen) == 2 and table["grad"].tolist() == [0, 0]
+    assert [st["step"] for st in states] == [7, 7] and steps.tolist() == [7, 7]
+    ps[1].grad = g1
+    status[0] = 0
+    assert step(groups) == 0 and seen[-1][6] == [7, 7] and [st["step"] for st in states] == [8, 8]
+    with pytest.raises(ValueError):
+        core.step(groups, table.ctypes.data, table.itemsize, cols, steps.ctypes.data, 0, 0x1234, 0x5678)
+
+
 def test_kernel_weight_decay_reproduces_torch_float32_factor():
     """_kernel_weight_decay: for a float32 tensor lr, the kernels' double expression
     (float)(1 - lr * wd') equals torch's float32 factor 1 - lr * wd for every
