@@ -40,6 +40,12 @@ template <> struct Conv<bf16_t> {
 };
 template <> struct Conv<f16_t> {
     __device__ __forceinline__ static f16_t from(float v) {
+        // v is a float32 result that is rounded to half here.  The empty asm keeps
+        // the backend from folding the operation that produced v into the
+        // conversion (v_fma_mixlo_f16 rounds a * b + c to half once, which differs
+        // from the float32 result rounded to half where that result is a half
+        // midpoint: p * (1 - lr * wd) of a half p is one such case).
+        __asm__("" : "+v"(v));
         f16_t r;
         const float a = fabsf(v);
         if (a < 6.103515625e-05f) {
