@@ -194,3 +194,91 @@ def test_random_batched_steps_match_oracle_and_plan(seed):
                   "16-bit parameters beyond one ulp (vmean rounding)", flush=True)
     finally:
         lib.gefen_step_plan_destroy(plan)
+
+
+@pytest.mark.parametrize("seed", [11, 2026])
+def test_random_muon_momentum_tasks_match_oracle(seed):
+    """GefenMuon's quantised momentum (gefen_muon_tasks) over 100 tensors of random
+    dtype pairs, block lengths, momentum and Nesterov settings in one call per
+    step: indices, magnitudes and the Nesterov / momentum output bit-exact
+    against the oracle (gefen_muon.py:216-260 on the CPU path) over 4 steps."""
+    rng = np.random.default_rng(seed)
+    cb = _codebook()
+    lib = _lib.load()
+    tables = torch.empty(int(lib.gefen_codebook_tables_size()), dtype=torch.uint8, device="cuda:0")
+    cb_dev = torch.from_numpy(cb).to("cuda:0")
+    _lib.check(lib.gefen_prepare_codebook(cb_dev.data_ptr(), cb.size, tables.data_ptr(), gu.stream()))
+    specs, ref, dev = [], [], []
+    for i in range(100):
+        dt, sdt = PAIRS[rng.integers(len(PAIRS))]
+        block = int(PERIODS[rng.integers(len(PERIODS))]) if rng.random() < 0.8 else int(rng.integers(1, 257))
+        n = block * int(rng.integers(1, max(2, 30000 // block)))
+        e_lo = int(rng.integers(-20, -7))
+        specs.append({"dt": dt, "sdt": sdt, "n": n, "block": block, "mom": float(rng.uniform(0.8, 0.99)),
+                      "nest": int(rng.integers(2)), "e_lo": e_lo, "e_hi": e_lo + int(rng.integers(2, 11))})
+        ref.append({"idx": np.zeros(n, np.uint8), "mag": np.zeros(n // block, orc.NP_STORAGE[sdt])})
+        dev.append({"g": torch.empty(n, dtype=gu.TORCH[dt], device="cuda:0"),
+                    "idx": torch.zeros(n, dtype=torch.uint8, device="cuda:0"),
+                    "mag": torch.zeros(n // block, dtype=gu.TORCH[sdt], device="cuda:0"),
+                    "out": torch.empty(n, dtype=gu.TORCH[dt], device="cuda:0")})
+    print("seed", seed, "muon tasks", len(specs), "elements", sum(s["n"] for s in specs), flush=True)
+    tasks = np.zeros(len(specs), dtype=_lib.MUON_TASK)
+    for t, s, d in zip(tasks, specs, dev):
+        t["grad"], t["m_codebook"], t["m_magnitude"] = d["g"].data_ptr(), d["idx"].data_ptr(), d["mag"].data_ptr()
+        t["out"], t["numel"], t["block"] = d["out"].data_ptr(), s["n"], s["block"]
+        t["grad_dtype"], t["state_dtype"] = gu.CODE[s["dt"]], gu.CODE[s["sdt"]]
+        t["momentum"], t["nesterov"] = s["mom"], s["nest"]
+    for step in range(1, STEPS + 1):
+        grads = []
+        for i, s in enumerate(specs):
+            g = _host(syn.round_to(syn.row_scaled_normal(seed * 1000 + i, step, s["n"] // s["block"], s["block"],
+                                                         s["e_lo"], s["e_hi"]), s["dt"]).reshape(-1).copy())
+            grads.append(g)
+            dev[i]["g"].copy_(gu.to_dev(g, s["dt"]))
+        _lib.check(lib.gefen_muon_tasks(tasks.ctypes.data, len(tasks), tables.data_ptr(), gu.stream()))
+        torch.cuda.synchronize()
+        for i, s in enumerate(specs):
+            r, d = ref[i], dev[i]
+            out = np.empty(s["n"], dtype=orc.NP_STORAGE[s["dt"]])
+            assert orc.lib().orc_muon_momentum(gu.CODE[s["dt"]], gu.CODE[s["sdt"]], orc._ptr(grads[i]),
+                                               orc._ptr(r["idx"]), orc._ptr(r["mag"]), orc._ptr(out), s["n"],
+                                               s["block"], orc._ptr(cb), cb.size, s["mom"], s["nest"]) == 0
+            tag = "muon task {} {}/{} n={} block={} step {}".format(i, s["dt"], s["sdt"], s["n"], s["block"], step)
+            np.testing.assert_array_equal(gu.to_np(d["idx"]), r["idx"], err_msg=tag + " idx")
+            np.testing.assert_array_equal(gu.to_np(d["mag"]), r["mag"], err_msg=tag + " mag")
+            np.testing.assert_array_equal(gu.to_np(d["out"]), out, err_msg=tag + " out")
+        print("step", step, "all", len(specs), "momentum tasks match the oracle", flush=True)
+
+
+@pytest.mark.parametrize("seed", [5, 77])
+def test_random_muon_apply_tasks_match_oracle(seed):
+    """GefenMuon's parameter update (gefen_muon_apply_tasks) over 60 parameters of
+    random dtypes, shapes (tall ones take the transposed-update rounding), lr,
+    weight decay and adjusted lr in one call: bit-exact against oracle.muon_apply
+    (gefen_muon.py:325-329 on the CPU path)."""
+    rng = np.random.default_rng(seed)
+    lib = _lib.load()
+    specs, dev, ref = [], [], []
+    for i in range(60):
+        dt = ["bf16", "bf16", "f16", "f32"][rng.integers(4)]
+        rows, cols = int(rng.integers(1, 300)), int(rng.integers(1, 300))
+        lr = float(10.0 ** rng.uniform(-4, -1.5))
+        wd = 0.0 if rng.random() < 0.4 else float(rng.uniform(0.01, 0.3))
+        adj = lr * float(rng.uniform(0.2, 3.0))
+        p = _host(syn.round_to(syn.normal(syn.make_key(seed, i), rows * cols) * 0.05, dt))
+        u = syn.round_to(syn.normal(syn.make_key(seed + 1, i), rows * cols), "bf16")
+        specs.append({"dt": dt, "shape": (rows, cols), "lr": lr, "wd": wd, "adj": adj, "u": u})
+        ref.append(p.copy())
+        dev.append({"p": gu.to_dev(p, dt), "u": gu.to_dev(u, "bf16")})
+    tasks = np.zeros(len(specs), dtype=_lib.MUON_APPLY_TASK)
+    for t, s, d in zip(tasks, specs, dev):
+        t["p"], t["update"], t["numel"] = d["p"].data_ptr(), d["u"].data_ptr(), s["shape"][0] * s["shape"][1]
+        t["param_dtype"], t["transposed"] = gu.CODE[s["dt"]], 1 if s["shape"][0] > s["shape"][1] else 0
+        t["lr"], t["weight_decay"], t["adjusted_lr"] = s["lr"], s["wd"], s["adj"]
+    _lib.check(lib.gefen_muon_apply_tasks(tasks.ctypes.data, len(tasks), gu.stream()))
+    torch.cuda.synchronize()
+    for i, s in enumerate(specs):
+        orc.muon_apply(ref[i], s["u"], s["dt"], s["shape"], s["lr"], s["wd"], s["adj"])
+        np.testing.assert_array_equal(gu.to_np(dev[i]["p"]), ref[i],
+                                      err_msg="apply task {} {} {}".format(i, s["dt"], s["shape"]))
+    print("seed", seed, "all", len(specs), "parameter updates match the oracle", flush=True)
