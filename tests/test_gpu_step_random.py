@@ -66,20 +66,6 @@ def _host(x):
     return x.view(np.uint16) if x.dtype == np.float16 else x
 
 
-def _ulp16(bits, dt):
-    if dt == "bf16":
-        return orc.ulp_bf16(bits)
-    return np.abs(np.spacing(bits.view(np.float16).astype(np.float16))).astype(np.float64)
-
-
-def _ulps(a, b):
-    a = a.astype(np.int32)
-    b = b.astype(np.int32)
-    ka = np.where(a & 0x8000, 0x8000 - (a & 0x7FFF), 0x8000 + (a & 0x7FFF))
-    kb = np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + (b & 0x7FFF))
-    return np.abs(ka - kb)
-
-
 def _task_rows(specs, dev):
     tasks = np.zeros(len(specs), dtype=_lib.STEP_TASK)
     for t, s, d in zip(tasks, specs, dev):
@@ -176,19 +162,19 @@ def test_random_batched_steps_match_oracle_and_plan(seed):
                 if sdt == "f32":
                     np.testing.assert_allclose(gv, r["v"], rtol=2.0 ** -18, atol=0, err_msg=tag + " vmean")
                 else:
-                    dv = _ulps(gv, r["v"])
+                    dv = gu.ulps16(gv, r["v"])
                     assert dv.max() <= 1, tag + " vmean"
                     r["flag"] |= dv == 1
                 if dt == "f32":
                     np.testing.assert_allclose(gp, r["p"], rtol=1e-5, atol=1e-7, err_msg=tag + " params")
                     continue
-                dp = _ulps(gp, r["p"])
+                dp = gu.ulps16(gp, r["p"])
                 far = np.nonzero(dp > 1)[0]
                 if far.size:
                     assert np.all(r["flag"][far // period]), (tag, far[:8])
                     diff = np.abs(orc.to_f32(gp[far], dt).astype(np.float64) -
                                   orc.to_f32(r["p"][far], dt).astype(np.float64))
-                    assert np.all(diff <= 2.0 ** -7 * r["moved"][far] + step * _ulp16(r["p"][far], dt)), (tag, far[:8])
+                    assert np.all(diff <= 2.0 ** -7 * r["moved"][far] + step * gu.ulp_at16(r["p"][far], dt)), (tag, far[:8])
                     beyond += far.size
             print("step", step, "all", len(specs), "tasks match the oracle;", beyond,
                   "16-bit parameters beyond one ulp (vmean rounding)", flush=True)
