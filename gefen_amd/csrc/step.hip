@@ -71,6 +71,17 @@ __global__ __launch_bounds__(256) void k_build_lut(float* __restrict__ lut, Step
     }
 }
 
+// Stepsize of each block from a given vmean of another dtype than the
+// magnitudes (gefen_automatic_fused_update_from_vmean): the expression the
+// given-vmean kernels evaluate on to_f32(vmean), so the given-stepsize update
+// that follows gives their results.
+template <typename V>
+__global__ __launch_bounds__(256) void k_block_stepsize(const V* __restrict__ vm, int64_t n, StepTask T,
+                                                        float* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = stepsize_of(to_f32(vm[i]), T);
+}
+
 // ---------------------------------------------------------------------------
 // vmean only (automatic_vmean_update): one lane group per row, streaming.
 template <typename G, typename S>
@@ -998,9 +1009,49 @@ static int single_update(void* p, const void* grad, int param_dtype, uint8_t* m_
     if (!valid_dtype(param_dtype)) return fail_inval("unsupported parameter dtype %d", param_dtype);
     if (!valid_pair(param_dtype, mag_dtype))
         return fail_inval("Expected m_magnitude to be float32, float16, or bfloat16 matching the parameters");
-    if (mode != kStepsizeGiven && vmean_dtype != mag_dtype)
-        return fail_inval("vmean dtype %d must match m_magnitude dtype %d", vmean_dtype, mag_dtype);
+    if (mode != kStepsizeGiven && !valid_dtype(vmean_dtype))
+        return fail_inval("Expected vmean to be float32, float16, or bfloat16, got %d", vmean_dtype);
+    if (mode == kVmeanUpdate && vmean_dtype != mag_dtype)
+        return fail_inval("the period-one update keeps vmean in the magnitude dtype: vmean dtype %d, "
+                          "m_magnitude dtype %d", vmean_dtype, mag_dtype);
     if (num_blocks < 0 || period <= 0) return fail_inval("Expected a positive period, got %lld", (long long)period);
+    if (mode == kVmeanGiven && vmean_dtype != mag_dtype && num_blocks > 0) {
+        // a vmean of another dtype: each block's stepsize formed on the device, then
+        // the given-stepsize update (the stepsize is all the kernels take from vmean)
+        if (bc1 <= 0.0 || bc2 <= 0.0 || !(eps >= 0.0)) return fail_inval("invalid bias corrections or eps");
+        if (!vmean) return fail_inval("null vmean");
+        gefen_step_task in;
+        memset(&in, 0, sizeof(in));
+        in.beta1 = beta1;
+        in.lr = lr;
+        in.eps = eps;
+        in.bias_correction_1 = bc1;
+        in.bias_correction_2 = bc2;
+        StepTask ts;
+        memset(&ts, 0, sizeof(ts));
+        set_step_scalars(in, ts);
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        void* tmp = nullptr;
+        hipError_t e = device_malloc_async(&tmp, (size_t)num_blocks * sizeof(float), st);
+        if (e != hipSuccess) return hip_status(e, "hipMallocAsync(block stepsizes)");
+        const unsigned grid = (unsigned)std::min<int64_t>((num_blocks + 255) / 256, 4096);
+        float* ss = static_cast<float*>(tmp);
+        if (vmean_dtype == GEFEN_F32)
+            hipLaunchKernelGGL(k_block_stepsize<float>, dim3(grid), dim3(256), 0, st, static_cast<const float*>(vmean),
+                               num_blocks, ts, ss);
+        else if (vmean_dtype == GEFEN_BF16)
+            hipLaunchKernelGGL(k_block_stepsize<bf16_t>, dim3(grid), dim3(256), 0, st,
+                               static_cast<const bf16_t*>(vmean), num_blocks, ts, ss);
+        else
+            hipLaunchKernelGGL(k_block_stepsize<f16_t>, dim3(grid), dim3(256), 0, st,
+                               static_cast<const f16_t*>(vmean), num_blocks, ts, ss);
+        rc = launch_status("gefen block stepsize");
+        if (rc == GEFEN_OK)
+            rc = single_update(p, grad, param_dtype, m_sign, mag, mag_dtype, nullptr, mag_dtype, ss, codebook, K,
+                               packed, num_blocks, period, 0, kStepsizeGiven, beta1, 0.0, lr, 1.0, 1.0, 0.0, stream);
+        (void)hipFreeAsync(tmp, st);
+        return rc;
+    }
     gefen_step_task t;
     memset(&t, 0, sizeof(t));
     t.p = p;

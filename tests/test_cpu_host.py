@@ -45,9 +45,14 @@ def test_entry_points_reject_invalid_arguments_without_a_device():
         _lib.check(lib.gefen_exact_histogram(1, 0, 16, 4, 1, 5000, None))
     with pytest.raises(ValueError, match="divisible"):
         _lib.check(lib.gefen_exact_histogram(1, 0, 17, 4, 1, 4096, None))
-    with pytest.raises(ValueError, match="vmean dtype"):
-        _lib.check(lib.gefen_automatic_fused_update_from_vmean(1, 1, 0, 1, 1, 0, 1, 1, 1, 256, 1, 4, 4, 0.9, 1e-3,
+    with pytest.raises(ValueError, match="Expected vmean to be float32"):
+        _lib.check(lib.gefen_automatic_fused_update_from_vmean(1, 1, 0, 1, 1, 0, 1, 7, 1, 256, 1, 4, 4, 0.9, 1e-3,
                                                                0.5, 0.5, 1e-8, None))
+    # a vmean of another dtype than the magnitudes is taken by the given-vmean
+    # entry point, not by the period-one update, whose kernels keep both in one dtype
+    with pytest.raises(ValueError, match="vmean dtype 1, m_magnitude dtype 0"):
+        _lib.check(lib.gefen_automatic_period1_update(1, 1, 0, 1, 1, 0, 1, 1, 1, 256, 16, 4, 0.9, 0.999, 1e-3,
+                                                      0.5, 0.5, 1e-8, None))
     with pytest.raises(ValueError, match="beta2"):
         _lib.check(lib.gefen_automatic_vmean_update(1, 0, 1, 0, 4, 4, 1.5, None))
     # the batched Newton-Schulz GEMM addresses a 256-row operand tile with 32-bit
