@@ -276,11 +276,15 @@ class GefenMuon(Gefen):
         _lib.check(rc, "gefen_muon_apply_tasks")
         for local_p, target in copy_back:
             local_p.copy_(target)
-        plain = (not copy_back and len(where) == len(items)
+        plain = (not copy_back
                  and all(local_p is p and grad is p.grad and grad.is_contiguous() for (_, p, local_p, grad) in items))
         if plain:
+            # matrices off the batched path keep their momentum output buffer and take
+            # the one-matrix Newton-Schulz in every run
+            solo = [(i, outs[i], tuple(items[i][0]["ns_coefficients"]), items[i][0]["ns_steps"], items[i][0]["eps"])
+                    for i in range(len(items)) if i not in where]
             self._plan = _MuonPlan(self, items, tasks, apply, [(key, idx, bufs[key], works[key], sum_index.get(key))
-                                                                 for key, idx in stacks.items()], dev, sumsq)
+                                                                 for key, idx in stacks.items()], dev, sumsq, solo)
         del keep
 
     @_step_entry
@@ -310,9 +314,11 @@ class _MuonPlan:
     A stack with Newton-Schulz steps applies its parameters' updates inside its
     last product (gefen_gemm_bf16_nt_batched_apply), so the updates are never
     stored and read back; the first step (the table build) applies them with
-    gefen_muon_apply_tasks, which the plan's results equal bit for bit."""
+    gefen_muon_apply_tasks, which the plan's results equal bit for bit.  Matrices
+    off the batched path keep their momentum output buffer and take the
+    one-matrix Newton-Schulz and gefen_muon_apply_tasks, as in the build."""
 
-    def __init__(self, opt, items, mtasks, apply, stacks, device, sumsq):
+    def __init__(self, opt, items, mtasks, apply, stacks, device, sumsq, solo=()):
         self.params = [it[1] for it in items]
         self.pptr = [it[1].data_ptr() for it in items]
         self.numel = [it[3].numel() for it in items]
@@ -343,6 +349,9 @@ class _MuonPlan:
             if ok:
                 fused[idx] = True
         self.rest = np.nonzero(~fused)[0]
+        # (item, momentum output, coefficients, steps, eps) of the matrices outside
+        # the stacks: one-matrix Newton-Schulz, then gefen_muon_apply_tasks
+        self.solo = [(i, out.view(items[i][3].shape), c, st, e) for i, out, c, st, e in solo]
         self.sumsq = sumsq
         self.settings = self._settings()
         self.core = None if _gefen_host is None else _gefen_host.PlanCore(self.params, self.states, self.state_keys)
@@ -411,6 +420,10 @@ class _MuonPlan:
                 keep.append((x, res))
                 slot_bytes = res[0].numel() * res.element_size()
                 self.apply["update"][idx] = res.data_ptr() + np.arange(len(idx), dtype=np.uint64) * slot_bytes
+            for i, out, coeffs, steps, eps in self.solo:
+                upd = _zeropower_via_newtonschulz(out, coeffs, steps, eps).contiguous()
+                keep.append(upd)
+                self.apply["update"][i] = upd.data_ptr()
             if len(self.rest):
                 rest = np.ascontiguousarray(self.apply[self.rest])
                 _lib.check(lib.gefen_muon_apply_tasks(rest.ctypes.data, len(rest), stream), "gefen_muon_apply_tasks")

@@ -125,7 +125,7 @@ def test_gefen_cached_plan_equals_full_steps(seed):
 def test_gefen_muon_cached_plan_equals_full_steps(seed):
     from gefen_amd.gefen_muon import GefenMuon
 
-    # every matrix on the batched Newton-Schulz path (a plan is kept only then)
-    shapes = [(256, 512), (512, 256), (256, 512), (256, 256), (256, 768), (768, 256)]
-    dtypes = ["bf16", "bf16", "bf16", "f32", "bf16", "bf16"]
+    # stacks of the batched Newton-Schulz path and two matrices off it (one-matrix path)
+    shapes = [(256, 512), (512, 256), (256, 512), (256, 256), (96, 200), (768, 256), (300, 64)]
+    dtypes = ["bf16", "bf16", "bf16", "f32", "bf16", "bf16", "f32"]
     _run("muon", seed, shapes, dtypes, GefenMuon, lr=2e-3, weight_decay=0.01)
