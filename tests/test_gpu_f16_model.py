@@ -61,7 +61,6 @@ def test_float16_gpt2_blocks_match_oracle_over_ten_steps():
     ref = orc.GefenOracle(arrs, codebook=ref_cb)
     moved = [np.zeros(a["p"].size) for a in arrs]
     flags = [np.zeros(n, bool) for n in (opt.state[p]["vmean"].numel() for _, p in params)]
-    total_far = 0
     for step in range(1, STEPS + 1):
         if step > 1:
             for i, (_, p) in enumerate(params):
@@ -99,6 +98,5 @@ def test_float16_gpt2_blocks_match_oracle_over_ten_steps():
                 far_step += far.size
         total = sum(a["p"].size for a in arrs)
         assert far_step <= 1e-3 * total, (step, far_step)
-        total_far = max(total_far, far_step)
         print("step", step, "all", len(params), "tensors match the oracle;", far_step, "of", total,
               "elements beyond one ulp (vmean rounding)", flush=True)
