@@ -166,7 +166,8 @@ def _special_codebook(kind):
 def test_step_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, period):
     """The two-probe search (dense), the general search (many thresholds per
     cell, thresholds below -1, duplicate codewords) and rows whose magnitude is
-    0, inf or NaN."""
+    0, inf or NaN: indices and magnitudes bit-exact, vmean and parameters NaN
+    exactly where the oracle's are and otherwise within the usual bounds."""
     print("case", kind, dt, period, flush=True)
     cb = _special_codebook(kind)
     n = (period if period > 1 else 256) * 16
@@ -206,6 +207,19 @@ def test_step_with_unusual_codebooks_and_nonfinite_gradients(kind, dt, period):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(gu.to_np(idx_dev), st_np["idx"], err_msg="idx step {}".format(step))
         np.testing.assert_array_equal(gu.to_np(mag_dev), st_np["mag"], err_msg="mag step {}".format(step))
+        # vmean and parameters, NaN where the oracle has NaN (any payload), else as in _run_case
+        for what, got, want in (("vmean", gu.to_np(v_dev), st_np["v"]), ("params", gu.to_np(p_dev), p_np)):
+            gf, wf = orc.to_f32(got, dt), orc.to_f32(want, dt)
+            tag = "{} step {}".format(what, step)
+            np.testing.assert_array_equal(np.isnan(gf), np.isnan(wf), err_msg=tag + " NaN positions")
+            ok = ~np.isnan(wf)
+            if period == 1:
+                np.testing.assert_array_equal(gf[ok], wf[ok], err_msg=tag)
+            elif dt == "f32":
+                np.testing.assert_allclose(gf[ok], wf[ok], rtol=1e-5 if what == "params" else 2.0 ** -18,
+                                           atol=1e-7 if what == "params" else 0, err_msg=tag)
+            else:
+                assert _ulps(got[ok], want[ok]).max(initial=0) <= 1, tag
 
 
 def test_misaligned_views_take_the_scalar_path():
