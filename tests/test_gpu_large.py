@@ -2,7 +2,8 @@
 its own magnitude block, the codebook and scalars, so the last blocks of a tensor
 of more than 2^31 elements, stepped inside it, must equal the same blocks stepped
 as a tensor of their own -- bit for bit, through two steps -- and every tensor of
-the full 8B-shaped step must equal itself stepped alone."""
+the full 8B-shaped step must equal itself stepped alone.  The first-step
+histogram of such a tensor is the sum of its parts' histograms."""
 
 import numpy as np
 import pytest
@@ -167,3 +168,23 @@ def test_full_qwen3_muon_momentum_equals_its_tensors_stepped_alone():
         assert torch.equal(st["m_codebook"], s["idx"])
         assert torch.equal(st["m_magnitude"].view(torch.int16), s["mag"].view(torch.int16))
     assert periods == {True, False}, periods
+
+
+def test_histogram_past_2_31_elements_is_the_sum_of_its_parts():
+    """The first-step histogram normalises each row by its own absmax, so the
+    counts of a tensor of more than 2^31 elements equal the counts of its first
+    2^31 elements plus those of the rest, each taken as a tensor of its own."""
+    print("large histogram", flush=True)
+    n = 2048 * (2 ** 20 + 64)
+    head = 2 ** 31
+    g = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
+    syn.fill_device(g, 41, 3, syn.KIND_ROW_SCALED, cols=2048, e_lo=-17, e_hi=-7)
+    lib = _lib.load()
+    counts = [torch.zeros(4096, dtype=torch.int64, device="cuda:0") for _ in range(3)]
+    for c, (start, stop) in zip(counts, [(0, n), (0, head), (head, n)]):
+        part = g[start:stop]
+        _lib.check(lib.gefen_exact_histogram(part.data_ptr(), gu.CODE["bf16"], stop - start, 2048, c.data_ptr(),
+                                             4096, gu.stream()))
+    torch.cuda.synchronize()
+    assert int(counts[0].sum()) == n
+    assert torch.equal(counts[0], counts[1] + counts[2])
