@@ -42,3 +42,10 @@ def test_bench_line_for_a_small_config():
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
     assert 0 < roof["frac"] == pytest.approx(roof["achieved"] / roof["peak"], abs=1e-4)
     assert out["config"]["tensors"] == 111 and sum(out["config"]["periods"].values()) == 111
+    # the step's timing split: launches inside step(), host time, the C calls
+    for key in ("kernel_ms_per_step", "step_frac", "frac_back_to_back", "copy_kernel_gbs", "host_ms_per_step",
+                "gpu_ms_outside_launches", "host_ms_plan_run", "host_ms_step_tasks"):
+        assert roof[key] > 0, key
+    assert roof["kernel_ms_per_step"] < out["ms_per_step"]
+    assert roof["step_frac"] == pytest.approx(roof["algorithmic_bytes_per_step"] / (out["ms_per_step"] * 1e-3) / 1e9
+                                              / roof["peak"], abs=1e-3)
